@@ -1,0 +1,131 @@
+// Internal host-side plumbing for libmarin_hip: errors, the device context, buffers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "marin_hip.h"
+
+namespace marin {
+
+// A failure carrying the marin_status and the fields of the matching reference error variant
+// (crates/cuda/src/error.rs:6-36).
+struct Error : std::runtime_error {
+    marin_status status;
+    size_t expected = 0, actual = 0, extra = 0;
+    bool oom = false;
+    Error(marin_status s, const std::string &msg, size_t e = 0, size_t a = 0, size_t x = 0)
+        : std::runtime_error(msg), status(s), expected(e), actual(a), extra(x) {}
+};
+
+[[noreturn]] inline void shape(const char *what, size_t expected, size_t actual) {
+    throw Error(MARIN_SHAPE,
+                std::string(what) + ": expected " + std::to_string(expected) + ", got " + std::to_string(actual),
+                expected, actual);
+}
+[[noreturn]] inline void unsupported(const char *what, size_t max, size_t actual) {
+    throw Error(MARIN_UNSUPPORTED,
+                std::string(what) + " must be between 1 and " + std::to_string(max) + ", got " +
+                    std::to_string(actual),
+                max, actual);
+}
+[[noreturn]] inline void overflow(const char *what) {
+    throw Error(MARIN_OVERFLOW, std::string(what) + ": size arithmetic overflowed");
+}
+inline void check_len(const char *what, size_t expected, size_t actual) {
+    if (expected != actual) shape(what, expected, actual);
+}
+inline size_t mul(size_t a, size_t b, const char *what) {
+    size_t r;
+    if (__builtin_mul_overflow(a, b, &r)) overflow(what);
+    return r;
+}
+inline uint32_t to_u32(size_t v, const char *what) {
+    if (v > 0xffffffffull) overflow(what);
+    return (uint32_t)v;
+}
+
+inline void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) {
+        Error err(MARIN_DRIVER, std::string("HIP error in ") + what + ": " + hipGetErrorString(e));
+        err.oom = e == hipErrorOutOfMemory;
+        throw err;
+    }
+}
+#define HIP_CHECK(call) ::marin::hip_check((call), #call)
+
+// Error-to-status translation for every exported function.
+void set_error(const Error &e);
+void set_error(marin_status s, const std::string &msg);
+void clear_error();
+
+template <class F>
+marin_status guard(F &&f) {
+    try {
+        f();
+        return MARIN_OK;
+    } catch (const Error &e) {
+        set_error(e);
+        return e.status;
+    } catch (const std::bad_alloc &) {
+        set_error(MARIN_DRIVER, "host allocation failed");
+        return MARIN_DRIVER;
+    } catch (const std::exception &e) {
+        set_error(MARIN_DRIVER, e.what());
+        return MARIN_DRIVER;
+    }
+}
+
+size_t dtype_bytes(marin_dtype d);
+
+}  // namespace marin
+
+// Device memory with the context that owns it.
+struct marin_buffer {
+    marin_gpu *gpu = nullptr;
+    void *data = nullptr;
+    size_t len = 0;  // elements
+    marin_dtype dtype = MARIN_F32;
+    size_t bytes() const { return len * marin::dtype_bytes(dtype); }
+};
+
+struct marin_tokens {
+    marin_gpu *gpu = nullptr;
+    uint32_t *data = nullptr;
+    size_t capacity = 0;
+};
+
+struct marin_gpu {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int cu_count = 0;
+    std::string name, arch;
+    // Counters of crates/cuda/src/counters.rs:10-89.
+    marin_traffic traffic{};
+    // Workspace the quantized products use: the f16 split of the activations and the cross-block partial sums with
+    // their arrival counters (counters return to zero after every product, so they are cleared only once).
+    void *split = nullptr;
+    size_t split_bytes = 0;
+    float *partials = nullptr;
+    size_t partial_floats = 0;
+    unsigned *counters = nullptr;
+    size_t counter_count = 0;
+    // Pinned staging for small host->device copies (token ids, page addresses).
+    void *pinned = nullptr;
+    size_t pinned_bytes = 0;
+
+    void *alloc(size_t bytes, bool zero = true);
+    void release(void *p);
+    void upload(void *dst, const void *src, size_t bytes);  // synchronous with respect to the host data
+    void download(void *dst, const void *src, size_t bytes);
+    void ensure_split(size_t bytes);
+    void ensure_partials(size_t floats, size_t counters);
+    void *stage(const void *src, size_t bytes);  // copies into pinned memory; valid until the next stage()
+    void launched() { traffic.launches++; }
+};

@@ -1,0 +1,359 @@
+// Device context, buffers, events and error reporting of the C ABI (crates/cuda/src/gpu.rs, counters.rs, error.rs).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace marin {
+
+struct LastError {
+    std::string msg;
+    size_t expected = 0, actual = 0, extra = 0;
+    bool oom = false;
+};
+static thread_local LastError g_last;
+
+void set_error(const Error &e) {
+    g_last.msg = e.what();
+    g_last.expected = e.expected;
+    g_last.actual = e.actual;
+    g_last.extra = e.extra;
+    g_last.oom = e.oom;
+}
+void set_error(marin_status, const std::string &msg) {
+    g_last = LastError{};
+    g_last.msg = msg;
+}
+void clear_error() { g_last = LastError{}; }
+
+size_t dtype_bytes(marin_dtype d) {
+    switch (d) {
+        case MARIN_F32:
+        case MARIN_U32: return 4;
+        case MARIN_BF16:
+        case MARIN_F16: return 2;
+        case MARIN_U8: return 1;
+    }
+    return 4;
+}
+
+}  // namespace marin
+
+using namespace marin;
+
+void *marin_gpu::alloc(size_t bytes, bool zero) {
+    void *p = nullptr;
+    if (bytes == 0) bytes = 4;
+    hipError_t e = hipMalloc(&p, bytes);
+    hip_check(e, "hipMalloc");
+    traffic.allocations++;
+    if (zero) {
+        HIP_CHECK(hipMemsetAsync(p, 0, bytes, stream));
+    }
+    return p;
+}
+
+void marin_gpu::release(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+void marin_gpu::upload(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return;
+    // Pageable host memory: a blocking copy ordered after the stream's earlier work.
+    HIP_CHECK(hipStreamSynchronize(stream));
+    HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    traffic.uploads++;
+    traffic.upload_bytes += bytes;
+}
+
+void marin_gpu::download(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return;
+    HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream));
+    HIP_CHECK(hipStreamSynchronize(stream));
+    traffic.downloads++;
+    traffic.download_bytes += bytes;
+}
+
+void marin_gpu::ensure_split(size_t bytes) {
+    if (bytes <= split_bytes) return;
+    HIP_CHECK(hipStreamSynchronize(stream));
+    release(split);
+    split = nullptr;
+    split_bytes = 0;
+    split = alloc(bytes, true);
+    split_bytes = bytes;
+}
+
+void marin_gpu::ensure_partials(size_t floats, size_t count) {
+    if (floats > partial_floats) {
+        HIP_CHECK(hipStreamSynchronize(stream));
+        release(partials);
+        partials = nullptr;
+        partial_floats = 0;
+        partials = (float *)alloc(floats * 4, false);
+        partial_floats = floats;
+    }
+    if (count > counter_count) {
+        HIP_CHECK(hipStreamSynchronize(stream));
+        release(counters);
+        counters = nullptr;
+        counter_count = 0;
+        counters = (unsigned *)alloc(count * 4, true);
+        counter_count = count;
+    }
+}
+
+void *marin_gpu::stage(const void *src, size_t bytes) {
+    if (bytes > pinned_bytes) {
+        HIP_CHECK(hipStreamSynchronize(stream));
+        if (pinned) (void)hipHostFree(pinned);
+        pinned = nullptr;
+        pinned_bytes = 0;
+        size_t want = std::max<size_t>(bytes, 1 << 16);
+        HIP_CHECK(hipHostMalloc(&pinned, want, hipHostMallocDefault));
+        pinned_bytes = want;
+    } else {
+        // The previous staged copy must have left the pinned area before it is overwritten.
+        HIP_CHECK(hipStreamSynchronize(stream));
+    }
+    std::memcpy(pinned, src, bytes);
+    return pinned;
+}
+
+extern "C" {
+
+const char *marin_last_error(void) { return g_last.msg.c_str(); }
+void marin_last_error_fields(size_t *expected, size_t *actual, size_t *extra) {
+    if (expected) *expected = g_last.expected;
+    if (actual) *actual = g_last.actual;
+    if (extra) *extra = g_last.extra;
+}
+int marin_last_error_is_oom(void) { return g_last.oom ? 1 : 0; }
+
+marin_status marin_gpu_new(marin_gpu **out) {
+    return guard([&] {
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+            throw Error(MARIN_UNAVAILABLE, "no HIP device is visible");
+        hipDeviceProp_t prop;
+        HIP_CHECK(hipGetDeviceProperties(&prop, 0));
+        std::string arch = prop.gcnArchName;
+        if (arch.rfind("gfx950", 0) != 0)
+            throw Error(MARIN_UNAVAILABLE, "device 0 is " + arch + "; this library is built for gfx950 only");
+        HIP_CHECK(hipSetDevice(0));
+        auto *g = new marin_gpu();
+        g->device = 0;
+        g->cu_count = prop.multiProcessorCount;
+        g->name = prop.name;
+        g->arch = arch;
+        hipError_t e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete g;
+            hip_check(e, "hipStreamCreate");
+        }
+        *out = g;
+    });
+}
+
+void marin_gpu_free(marin_gpu *g) {
+    if (!g) return;
+    (void)hipStreamSynchronize(g->stream);
+    forget_rope_frequencies(g);
+    g->release(g->split);
+    g->release(g->partials);
+    g->release(g->counters);
+    if (g->pinned) (void)hipHostFree(g->pinned);
+    (void)hipStreamDestroy(g->stream);
+    delete g;
+}
+
+marin_status marin_gpu_info_get(marin_gpu *g, marin_gpu_info *out) {
+    return guard([&] {
+        std::memset(out, 0, sizeof(*out));
+        std::snprintf(out->name, sizeof(out->name), "%s", g->name.c_str());
+        std::snprintf(out->arch, sizeof(out->arch), "%s", g->arch.c_str());
+        out->compute_units = g->cu_count;
+        HIP_CHECK(hipMemGetInfo(&out->free_bytes, &out->total_bytes));
+    });
+}
+
+marin_status marin_gpu_synchronize(marin_gpu *g) {
+    return guard([&] { HIP_CHECK(hipStreamSynchronize(g->stream)); });
+}
+
+void *marin_gpu_stream(marin_gpu *g) { return (void *)g->stream; }
+
+marin_status marin_gpu_traffic(marin_gpu *g, marin_traffic *out) {
+    return guard([&] { *out = g->traffic; });
+}
+
+struct marin_mark {
+    hipEvent_t event;
+};
+
+marin_status marin_mark_new(marin_gpu *g, marin_mark **out) {
+    return guard([&] {
+        auto *m = new marin_mark();
+        hipError_t e = hipEventCreate(&m->event);
+        if (e != hipSuccess) {
+            delete m;
+            hip_check(e, "hipEventCreate");
+        }
+        HIP_CHECK(hipEventRecord(m->event, g->stream));
+        *out = m;
+    });
+}
+
+marin_status marin_mark_since(marin_mark *later, marin_mark *earlier, double *seconds) {
+    return guard([&] {
+        HIP_CHECK(hipEventSynchronize(later->event));
+        float ms = 0;
+        HIP_CHECK(hipEventElapsedTime(&ms, earlier->event, later->event));
+        *seconds = ms * 1e-3;
+    });
+}
+
+void marin_mark_free(marin_mark *m) {
+    if (!m) return;
+    (void)hipEventDestroy(m->event);
+    delete m;
+}
+
+static marin_buffer *new_buffer(marin_gpu *g, marin_dtype dtype, size_t len) {
+    auto *b = new marin_buffer();
+    b->gpu = g;
+    b->dtype = dtype;
+    b->len = len;
+    try {
+        b->data = g->alloc(b->bytes(), true);
+    } catch (...) {
+        delete b;
+        throw;
+    }
+    return b;
+}
+
+marin_status marin_buffer_zeros(marin_gpu *g, size_t len, marin_buffer **out) {
+    return guard([&] {
+        mul(len, 4, "buffer");
+        *out = new_buffer(g, MARIN_F32, len);
+    });
+}
+
+marin_status marin_buffer_upload(marin_gpu *g, const float *values, size_t len, marin_buffer **out) {
+    return guard([&] {
+        mul(len, 4, "buffer");
+        marin_buffer *b = new_buffer(g, MARIN_F32, len);
+        try {
+            g->upload(b->data, values, len * 4);
+        } catch (...) {
+            g->release(b->data);
+            delete b;
+            throw;
+        }
+        *out = b;
+    });
+}
+
+marin_status marin_buffer_upload_into(marin_gpu *g, const float *values, size_t len, marin_buffer *dst) {
+    return guard([&] {
+        check_len("upload length", dst->len, len);
+        g->upload(dst->data, values, len * 4);
+    });
+}
+
+marin_status marin_buffer_download(marin_gpu *g, const marin_buffer *b, float *dst, size_t len) {
+    return guard([&] {
+        if (b->dtype != MARIN_F32) shape("buffer element size", 4, dtype_bytes(b->dtype));
+        check_len("download length", b->len, len);
+        g->download(dst, b->data, len * 4);
+    });
+}
+
+marin_status marin_buffer_download_range(marin_gpu *g, const marin_buffer *b, size_t start, size_t len, float *dst) {
+    return guard([&] {
+        if (start > b->len || len > b->len - start) shape("download range", b->len, start + len);
+        g->download(dst, (const float *)b->data + start, len * 4);
+    });
+}
+
+marin_status marin_buffer_copy_range_into(marin_gpu *g, const marin_buffer *src, size_t start, marin_buffer *dst) {
+    return guard([&] {
+        if (start > src->len || dst->len > src->len - start) shape("copy range", src->len, start + dst->len);
+        if (!dst->len) return;
+        HIP_CHECK(hipMemcpyAsync(dst->data, (const float *)src->data + start, dst->len * 4,
+                                 hipMemcpyDeviceToDevice, g->stream));
+    });
+}
+
+marin_status marin_buffer_copy_into_range(marin_gpu *g, const marin_buffer *src, marin_buffer *dst, size_t start) {
+    return guard([&] {
+        if (start > dst->len || src->len > dst->len - start) shape("copy range", dst->len, start + src->len);
+        if (!src->len) return;
+        HIP_CHECK(hipMemcpyAsync((float *)dst->data + start, src->data, src->len * 4, hipMemcpyDeviceToDevice,
+                                 g->stream));
+    });
+}
+
+size_t marin_buffer_len(const marin_buffer *b) { return b->len; }
+marin_dtype marin_buffer_dtype(const marin_buffer *b) { return b->dtype; }
+void *marin_buffer_device_ptr(const marin_buffer *b) { return b->data; }
+
+void marin_buffer_free(marin_buffer *b) {
+    if (!b) return;
+    (void)hipStreamSynchronize(b->gpu->stream);
+    b->gpu->release(b->data);
+    delete b;
+}
+
+marin_status marin_buffer_new_typed(marin_gpu *g, marin_dtype dtype, size_t len, const void *host,
+                                    marin_buffer **out) {
+    return guard([&] {
+        mul(len, dtype_bytes(dtype), "buffer");
+        marin_buffer *b = new_buffer(g, dtype, len);
+        if (host) {
+            try {
+                g->upload(b->data, host, b->bytes());
+            } catch (...) {
+                g->release(b->data);
+                delete b;
+                throw;
+            }
+        }
+        *out = b;
+    });
+}
+
+marin_status marin_buffer_download_raw(marin_gpu *g, const marin_buffer *b, void *dst, size_t bytes) {
+    return guard([&] {
+        check_len("download bytes", b->bytes(), bytes);
+        g->download(dst, b->data, bytes);
+    });
+}
+
+marin_status marin_tokens_new(marin_gpu *g, size_t capacity, marin_tokens **out) {
+    return guard([&] {
+        auto *t = new marin_tokens();
+        t->gpu = g;
+        t->capacity = capacity;
+        try {
+            t->data = (uint32_t *)g->alloc(mul(std::max<size_t>(capacity, 1), 4, "tokens"), true);
+        } catch (...) {
+            delete t;
+            throw;
+        }
+        *out = t;
+    });
+}
+
+void marin_tokens_free(marin_tokens *t) {
+    if (!t) return;
+    (void)hipStreamSynchronize(t->gpu->stream);
+    t->gpu->release(t->data);
+    delete t;
+}
+
+}  // extern "C"

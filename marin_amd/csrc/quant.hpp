@@ -1,0 +1,75 @@
+// Quantized matrices on the device and the product kernels' launch interface.
+#pragma once
+
+#include "common.hpp"
+
+// Device layout of a quantized matrix (the reference keeps Quantized's layout, crates/cuda/src/quant.rs:16-23; this
+// backend keeps the codes byte for byte but stores the scales tiled for the MFMA product):
+//  codes  [rows_padded][row_bytes]   int8 two's complement, or int4 pairs (even column low nibble, +8)
+//  scales [rows_padded/16][groups][16]  f32 or bf16: the 16 rows of a tile side by side for each group, so a lane
+//         reads the scales of its four output rows with one 16-byte (8-byte) load.
+// Rows past `rows` up to the next multiple of 64 are zero codes with zero scales.
+struct marin_quant_matrix {
+    marin_gpu *gpu = nullptr;
+    size_t rows = 0, cols = 0, group = 0, rows_padded = 0;
+    int bits = 8;
+    bool bf16_scales = false;
+    uint8_t *codes = nullptr;
+    void *scales = nullptr;
+    size_t groups() const { return cols / group; }
+    size_t row_bytes() const { return bits == 8 ? cols : (cols + 1) / 2; }
+};
+
+namespace marin {
+
+constexpr size_t ROW_PAD = 64;
+constexpr int MAX_GEMV_TOKENS = 8;
+
+// f16 hi/lo split of activations: data [tokens][2][cols] then f32 inv[tokens] (the per-token power of two that undoes
+// the scaling applied before the split). The MFMA product reads its B operand from here.
+struct SplitView {
+    _Float16 *data;
+    float *inv;
+    size_t cols, tokens;
+};
+size_t split_bytes(size_t tokens, size_t cols);
+SplitView split_view(void *base, size_t tokens, size_t cols);
+
+enum Epilogue : int {
+    EPI_F32 = 0,        // y[t][r] = v
+    EPI_ADD = 1,        // y[t][r] += v (residual)
+    EPI_BF16 = 2,       // y bf16
+    EPI_SILU_SPLIT = 3  // rows (2i, 2i+1) = (gate_i, up_i): silu(gate)*up -> f16 split of [tokens][rows/2]
+};
+
+struct EpiArgs {
+    void *y = nullptr;       // EPI_F32/ADD/BF16: [tokens][y_stride]
+    size_t y_stride = 0;     // elements between tokens of y
+    SplitView split_out{};   // EPI_SILU_SPLIT
+    float *act_out = nullptr; // EPI_SILU_SPLIT: optional f32 copy [tokens][rows/2]
+};
+
+// Launchers (all on gpu->stream, no synchronization).
+void launch_split_f32(marin_gpu *g, const float *x, size_t tokens, size_t cols, SplitView out, bool scale_tokens);
+void launch_split_bf16(marin_gpu *g, const uint16_t *x, size_t tokens, size_t cols, SplitView out);
+bool mfma_supported(const marin_quant_matrix *w);
+void launch_gemv_mfma(marin_gpu *g, const marin_quant_matrix *w, SplitView x, size_t tokens, Epilogue epi,
+                      const EpiArgs &args);
+void launch_gemv_valu(marin_gpu *g, const marin_quant_matrix *w, const float *x, size_t tokens, float *y);
+void launch_embed_q8(marin_gpu *g, const marin_quant_matrix *w, const uint32_t *ids, size_t n, float *out);
+// Fills a matrix from the synthetic generator (seed, stream) and quantizes it int8 with the reference's rule.
+// rows_map: optional device-side row permutation: generated row r goes to device row map(r) (for fused layouts).
+void launch_synth_quantize(marin_gpu *g, marin_quant_matrix *w, uint64_t seed, uint64_t stream, double std_dev,
+                           size_t src_rows, size_t dst_row0, size_t dst_row_step);
+
+marin_quant_matrix *new_quant_matrix(marin_gpu *g, size_t rows, size_t cols, int bits, size_t group, bool bf16);
+void free_quant_matrix(marin_quant_matrix *m);
+// Host codes/scales (Quantized layout) -> device layout, rows placed from dst_row0 with stride dst_row_step.
+void upload_rows(marin_quant_matrix *m, const uint8_t *codes, const void *scales, size_t src_rows, size_t dst_row0,
+                 size_t dst_row_step);
+
+// The product every entry point takes: splits x into the workspace and runs the MFMA kernel when the matrix
+// allows, the VALU kernel otherwise. tokens may exceed MAX_GEMV_TOKENS (chunks of it).
+void matmul_f32(marin_gpu *g, const marin_quant_matrix *w, const float *x, size_t tokens, float *y, bool precise);
+
+}  // namespace marin
