@@ -234,6 +234,25 @@ marin_status marin_qwen3_forward(marin_qwen3 *m, marin_qwen3_cache *c, const uin
 marin_status marin_qwen3_generate(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *prompt, size_t n,
                                   size_t steps, uint32_t *tokens_out);
 
+/* Extension: continues greedy decoding for `steps` more tokens after a forward/generate on this cache (the
+ * choice from the last pass's logits is the first token written). */
+marin_status marin_qwen3_decode(marin_qwen3 *m, marin_qwen3_cache *c, size_t steps, uint32_t *tokens_out);
+/* Extension (measurement): one decode step like marin_qwen3_decode(steps = 1), with an event between every launch.
+ * Reports the summed durations and algorithmic bytes of the quantized products (weights + scales + activations +
+ * outputs) and of attention (keys + values read, queries, outputs), and the whole step. */
+typedef struct marin_step_profile {
+    double gemv_seconds, gemv_bytes;
+    double attention_seconds, attention_bytes;
+    double other_seconds, step_seconds;
+    uint32_t gemv_launches, attention_launches, other_launches;
+} marin_step_profile;
+marin_status marin_qwen3_profile_step(marin_qwen3 *m, marin_qwen3_cache *c, marin_step_profile *out);
+
+/* Extension: a rows x cols int8 matrix from the synthetic generator (seed, stream), N(0, std), quantized on the
+ * device with the reference's rule (tensor/src/quant.rs:181-234); the oracle restates both bit for bit. */
+marin_status marin_quantized_synthetic(marin_gpu *gpu, size_t rows, size_t cols, size_t group, uint64_t seed,
+                                       uint64_t stream, double std_dev, marin_quant_matrix **out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,7 +12,7 @@ import enum
 
 import numpy as np
 
-from ._lib import GpuInfo, TrafficC, lib
+from ._lib import GpuInfo, TrafficC, alive, lib
 
 PAGE_TOKENS = 64  # crates/cuda/src/pages.rs:4
 SLAB_PAGES = 8  # crates/cuda/src/pages.rs:7
@@ -126,7 +126,7 @@ class Buffer:
         return int(lib.marin_buffer_device_ptr(self._h) or 0)
 
     def free(self) -> None:
-        if self._h:
+        if self._h and alive():
             lib.marin_buffer_free(self._h)
             self._h = None
 
@@ -145,7 +145,7 @@ class Tokens:
         self.capacity = capacity
 
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and alive():
             lib.marin_tokens_free(self._h)
             self._h = None
 
@@ -169,7 +169,7 @@ class DeviceQuantMatrix:
         return int(lib.marin_quant_matrix_bytes(self._h))
 
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and alive():
             lib.marin_quant_matrix_free(self._h)
             self._h = None
 
@@ -192,7 +192,7 @@ class Mark:
         return s.value
 
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and alive():
             lib.marin_mark_free(self._h)
             self._h = None
 
@@ -214,7 +214,7 @@ class Gpu:
         return self._h
 
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and alive():
             lib.marin_gpu_free(self._h)
             self._h = None
 
@@ -307,6 +307,13 @@ class Gpu:
                                              scales.ctypes.data, scales.size, C.byref(h)))
         return DeviceQuantMatrix(h)
 
+    def quantized_synthetic(self, rows: int, cols: int, group: int, seed: int, stream: int,
+                            std: float = 0.02) -> DeviceQuantMatrix:
+        """A synthetic int8 matrix generated and quantized on the device (extension; see include/marin_hip.h)."""
+        h = _out()
+        check(lib.marin_quantized_synthetic(self._h, rows, cols, group, seed, stream, std, C.byref(h)))
+        return DeviceQuantMatrix(h)
+
     def embed_quant(self, table: DeviceQuantMatrix, ids, scratch: Tokens, out: Buffer) -> None:
         ids = np.ascontiguousarray(ids, np.uint32).ravel()
         check(lib.marin_embed_quant(self._h, table._h, ids.ctypes.data if ids.size else None, ids.size,
@@ -354,7 +361,7 @@ class DeviceKv:
         self.format = KvFormat(fmt)
 
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and alive():
             lib.marin_kv_free(self._h)
             self._h = None
 
@@ -416,7 +423,7 @@ class PagePool:
                                                                                    head_dim, KvFormat(fmt))
 
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and alive():
             lib.marin_page_pool_free(self._h)
             self._h = None
 

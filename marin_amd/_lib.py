@@ -26,6 +26,12 @@ class TrafficC(C.Structure):
                                           "download_bytes")]
 
 
+class StepProfileC(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("gemv_seconds", "gemv_bytes", "attention_seconds", "attention_bytes",
+                                          "other_seconds", "step_seconds")] + [
+        (n, C.c_uint32) for n in ("gemv_launches", "attention_launches", "other_launches")]
+
+
 class Qwen3ConfigC(C.Structure):
     _fields_ = [(n, sz) for n in ("layers", "hidden", "heads", "kv_heads", "head_dim", "ffn", "vocab")] + [
         ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("tie_embeddings", C.c_int), ("group", sz)]
@@ -104,10 +110,10 @@ SIGNATURES = {
     "marin_qwen3_cache_truncate": (st, [P, sz]),
     "marin_qwen3_forward": (st, [P, P, P, sz, P]),
     "marin_qwen3_generate": (st, [P, P, P, sz, sz, P]),
+    "marin_qwen3_decode": (st, [P, P, sz, P]),
+    "marin_qwen3_profile_step": (st, [P, P, C.POINTER(StepProfileC)]),
+    "marin_quantized_synthetic": (st, [P, sz, sz, sz, C.c_uint64, C.c_uint64, C.c_double, PP]),
 }
-
-
-PENDING = {n for n in SIGNATURES if n.startswith("marin_qwen3")}
 
 
 def load(path: str = LIB_PATH) -> C.CDLL:
@@ -117,8 +123,6 @@ def load(path: str = LIB_PATH) -> C.CDLL:
             "(there is no fallback path)")
     lib = C.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
-        if name in PENDING and not hasattr(lib, name):
-            continue
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
@@ -126,3 +130,14 @@ def load(path: str = LIB_PATH) -> C.CDLL:
 
 
 lib = load()
+
+# Once the interpreter is shutting down, handles are left to the process exit instead of being freed from __del__
+# in whatever order finalization reaches them.
+import atexit  # noqa: E402
+
+SHUTTING_DOWN = [False]
+atexit.register(lambda: SHUTTING_DOWN.__setitem__(0, True))
+
+
+def alive() -> bool:
+    return not SHUTTING_DOWN[0]

@@ -311,7 +311,7 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
         case MARIN_KV_F16: launch_partial_f<MARIN_KV_F16>(g, a, grid, chunk, splits, scale); break;
         default: launch_partial_f<MARIN_KV_BF16>(g, a, grid, chunk, splits, scale); break;
     }
-    g->launched();
+    g->launched(marin_gpu::ATTENTION, a.bytes_hint);
     const dim3 mgrid((unsigned)(a.batch * a.tokens * a.heads));
     const dim3 mblock((unsigned)std::min<size_t>(256, (a.geom.head_dim + 63) / 64 * 64));
     if (a.out_kind == 0)
@@ -323,7 +323,7 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     else
         attention_merge<2><<<mgrid, mblock, 0, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
                                                             (int)a.geom.head_dim, chunk, splits, a.out, a.split_inv);
-    g->launched();
+    g->launched(marin_gpu::ATTENTION, 0.0);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -74,6 +74,7 @@ struct AttentionArgs {
     float *partials;
     size_t partial_floats;
     float *split_inv;  // out_kind 2: where the per-token inverse scale goes
+    double bytes_hint = 0.0;  // algorithmic bytes, for launch accounting only
 };
 size_t attention_partial_floats(size_t batch, size_t tokens, size_t heads, size_t head_dim, size_t max_ctx,
                                 int cu_count);

@@ -120,12 +120,29 @@ struct marin_gpu {
     void *pinned = nullptr;
     size_t pinned_bytes = 0;
 
+    // Every device allocation made through alloc() holds the context: marin_gpu_free only marks it closing, and the
+    // context is destroyed when its last allocation is released (as the reference's buffers hold an Arc of their
+    // context), so objects may be freed in any order.
+    size_t live = 0;
+    bool closing = false;
     void *alloc(size_t bytes, bool zero = true);
     void release(void *p);
+    void destroy();
     void upload(void *dst, const void *src, size_t bytes);  // synchronous with respect to the host data
     void download(void *dst, const void *src, size_t bytes);
     void ensure_split(size_t bytes);
     void ensure_partials(size_t floats, size_t counters);
     void *stage(const void *src, size_t bytes);  // copies into pinned memory; valid until the next stage()
-    void launched() { traffic.launches++; }
+
+    // Launch accounting. With a profile attached, every launch records an event after itself, tagged with its kind
+    // and algorithmic bytes, so the gap between consecutive events is that kernel's time on the stream.
+    enum Kind { OTHER = 0, GEMV = 1, ATTENTION = 2 };
+    struct ProfileEntry {
+        hipEvent_t event;
+        int kind;
+        double bytes;
+    };
+    std::vector<ProfileEntry> *profile = nullptr;
+    std::vector<hipEvent_t> event_pool;
+    void launched(int kind = OTHER, double bytes = 0.0);
 };

@@ -50,6 +50,7 @@ void *marin_gpu::alloc(size_t bytes, bool zero) {
     hipError_t e = hipMalloc(&p, bytes);
     hip_check(e, "hipMalloc");
     traffic.allocations++;
+    live++;
     if (zero) {
         HIP_CHECK(hipMemsetAsync(p, 0, bytes, stream));
     }
@@ -57,7 +58,18 @@ void *marin_gpu::alloc(size_t bytes, bool zero) {
 }
 
 void marin_gpu::release(void *p) {
-    if (p) (void)hipFree(p);
+    if (!p) return;
+    (void)hipFree(p);
+    live--;
+    if (closing && live == 0) destroy();
+}
+
+void marin_gpu::destroy() {
+    (void)hipStreamSynchronize(stream);
+    if (pinned) (void)hipHostFree(pinned);
+    for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(stream);
+    delete this;
 }
 
 void marin_gpu::upload(void *dst, const void *src, size_t bytes) {
@@ -104,6 +116,19 @@ void marin_gpu::ensure_partials(size_t floats, size_t count) {
         counters = (unsigned *)alloc(count * 4, true);
         counter_count = count;
     }
+}
+
+void marin_gpu::launched(int kind, double bytes) {
+    traffic.launches++;
+    if (!profile) return;
+    const size_t i = profile->size();
+    if (i >= event_pool.size()) {
+        hipEvent_t e;
+        HIP_CHECK(hipEventCreate(&e));
+        event_pool.push_back(e);
+    }
+    HIP_CHECK(hipEventRecord(event_pool[i], stream));
+    profile->push_back({event_pool[i], kind, bytes});
 }
 
 void *marin_gpu::stage(const void *src, size_t bytes) {
@@ -159,15 +184,17 @@ marin_status marin_gpu_new(marin_gpu **out) {
 }
 
 void marin_gpu_free(marin_gpu *g) {
-    if (!g) return;
+    if (!g || g->closing) return;
     (void)hipStreamSynchronize(g->stream);
     forget_rope_frequencies(g);
     g->release(g->split);
+    g->split = nullptr;
     g->release(g->partials);
+    g->partials = nullptr;
     g->release(g->counters);
-    if (g->pinned) (void)hipHostFree(g->pinned);
-    (void)hipStreamDestroy(g->stream);
-    delete g;
+    g->counters = nullptr;
+    g->closing = true;
+    if (g->live == 0) g->destroy();
 }
 
 marin_status marin_gpu_info_get(marin_gpu *g, marin_gpu_info *out) {

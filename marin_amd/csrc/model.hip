@@ -1,0 +1,707 @@
+// The Qwen3 decode pass over this backend (model/src/qwen3/gpu.rs:222-377 Qwen3Gpu::pass, weight.rs, workspace.rs of
+// the reference), with MI355X-first fusion:
+//  - q, k and v are one matrix (rows q | k | v), so the three projections are one weight stream;
+//  - gate and up are interleaved row by row, so the GEMV epilogue sees (gate_i, up_i) in one lane and writes
+//    silu(gate) * up straight into the f16 split the down projection reads;
+//  - the o and down projections add into the residual stream in their epilogue;
+//  - q/k RMSNorm, RoPE and the KV-cache store are one kernel;
+//  - every norm writes the f16 split its GEMV consumes, and attention's merge writes o_proj's split.
+// Positions live in device memory (pos, ctx), so a decode step has no host arguments and replays as a HIP graph:
+// the greedy loop picks the next token on the device and feeds it back without a host round trip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <memory>
+
+#include "attention.hpp"
+#include "ops.hpp"
+#include "quant.hpp"
+
+using namespace marin;
+
+namespace marin {
+
+constexpr size_t CHUNK = MAX_GEMV_TOKENS;  // tokens per pass through the layers
+
+// RMSNorm of rows [row0, row0 + n) of x into the f16 split (per-token power-of-two scaling), one block per row.
+__global__ __launch_bounds__(256) void rms_norm_split_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                             int dim, float eps, _Float16 *__restrict__ data,
+                                                             float *__restrict__ inv) {
+    const int t = blockIdx.x;
+    const float *row = x + (size_t)t * dim;
+    __shared__ float red[4];
+    __shared__ float redm[4];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += 256) s += row[i] * row[i];
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = 1.0f / sqrtf(total / (float)dim + eps);
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += 256) m = fmaxf(m, fabsf(row[i] * scale * w[i]));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+    float up = 1.0f, down = 1.0f;
+    if (m > 0.0f && m < INFINITY) {
+        int e;
+        (void)frexpf(m, &e);
+        int sh = 15 - e;
+        sh = sh > 100 ? 100 : (sh < -100 ? -100 : sh);
+        up = ldexpf(1.0f, sh);
+        down = ldexpf(1.0f, -sh);
+    }
+    for (int i = threadIdx.x; i < dim; i += 256) {
+        const float y = row[i] * scale * w[i] * up;
+        const _Float16 hi = (_Float16)y;
+        data[((size_t)t * 2) * dim + i] = hi;
+        data[((size_t)t * 2 + 1) * dim + i] = (_Float16)(y - (float)hi);
+    }
+    if (threadIdx.x == 0) inv[t] = down;
+}
+
+// Per (token, head): q heads get RMSNorm(q_norm) + RoPE into q; k heads RMSNorm(k_norm) + RoPE into the cache; v heads
+// go to the cache as they are. grid (tokens, heads + 2 * kv_heads), 64 threads; thread i takes the pairs (i, i + hd/2).
+template <int F>
+__global__ __launch_bounds__(64) void qk_norm_rope_store(const float *__restrict__ qkv, float *__restrict__ q_out,
+                                                         const float *__restrict__ q_norm,
+                                                         const float *__restrict__ k_norm,
+                                                         const float *__restrict__ freq, const uint64_t *__restrict__ pages,
+                                                         KvGeom geom, const uint32_t *__restrict__ state, int heads,
+                                                         int kv_heads, float eps) {
+    const int t = blockIdx.x, j = blockIdx.y, lane = threadIdx.x;
+    const int hd = (int)geom.head_dim, half = hd / 2;
+    const int qd = heads * hd, kvd = kv_heads * hd;
+    const uint32_t pos = state[0] + t;
+    const float *src;
+    int kind, kvh = 0;
+    if (j < heads) {
+        kind = 0;
+        src = qkv + (size_t)t * (qd + 2 * kvd) + (size_t)j * hd;
+    } else if (j < heads + kv_heads) {
+        kind = 1;
+        kvh = j - heads;
+        src = qkv + (size_t)t * (qd + 2 * kvd) + qd + (size_t)kvh * hd;
+    } else {
+        kind = 2;
+        kvh = j - heads - kv_heads;
+        src = qkv + (size_t)t * (qd + 2 * kvd) + qd + kvd + (size_t)kvh * hd;
+    }
+    constexpr int MAXP = 2;  // head_dim <= 256
+    float a[MAXP], b[MAXP];
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) {
+        const int i = lane + 64 * k;
+        a[k] = i < half ? src[i] : 0.0f;
+        b[k] = i < half ? src[i + half] : 0.0f;
+    }
+    if (kind != 2) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) s += a[k] * a[k] + b[k] * b[k];
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+        const float scale = 1.0f / sqrtf(s / (float)hd + eps);
+        const float *w = kind == 0 ? q_norm : k_norm;
+        const float position = (float)pos;
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) {
+            const int i = lane + 64 * k;
+            if (i >= half) continue;
+            const float x = a[k] * scale * w[i], y = b[k] * scale * w[i + half];
+            float sn, cs;
+            sincosf(position * freq[i], &sn, &cs);
+            a[k] = x * cs - y * sn;
+            b[k] = y * cs + x * sn;
+        }
+    }
+    if (kind == 0) {
+        float *dst = q_out + (size_t)t * qd + (size_t)j * hd;
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) {
+            const int i = lane + 64 * k;
+            if (i < half) {
+                dst[i] = a[k];
+                dst[i + half] = b[k];
+            }
+        }
+        return;
+    }
+    const uint64_t page = pages[pos >> geom.page_shift];
+    const uint32_t in_page = pos & ((1u << geom.page_shift) - 1u);
+    const size_t es = F == MARIN_KV_F32 ? 4 : 2;
+    uint8_t *row = reinterpret_cast<uint8_t *>(page + geom.layer_offset + (kind == 2 ? geom.value_offset : 0) +
+                                               (uint64_t)kvh * geom.head_bytes + (uint64_t)in_page * hd * es);
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) {
+        const int i = lane + 64 * k;
+        if (i >= half) continue;
+        const float vals[2] = {a[k], b[k]};
+        const int idx[2] = {i, i + half};
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const float x = vals[u];
+            if constexpr (F == MARIN_KV_F32) reinterpret_cast<float *>(row)[idx[u]] = x;
+            if constexpr (F == MARIN_KV_F16) {
+                const float c = fminf(fmaxf(x, -65504.0f), 65504.0f);
+                reinterpret_cast<_Float16 *>(row)[idx[u]] = (_Float16)(x != x ? x : c);
+            }
+            if constexpr (F == MARIN_KV_BF16) {
+                const unsigned uu = __float_as_uint(x);
+                reinterpret_cast<uint16_t *>(row)[idx[u]] =
+                    (uint16_t)((uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
+                                                                : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+            }
+        }
+    }
+}
+
+// Greedy choice (sampler/src/lib.rs:40-48): the largest logit under f32's total order, the lowest id on ties. One
+// block; the winner goes to ids[0] (the next pass's input) and to tokens_out[step] with step = state[2]. Then the
+// state advances: pos += count, ctx = pos + 1, step += 1.
+__device__ __forceinline__ int total_key(float v) {
+    const int b = __float_as_int(v);
+    return b ^ (int)(((unsigned)(b >> 31)) >> 1);
+}
+
+__global__ __launch_bounds__(1024) void argmax_advance(const float *__restrict__ logits, int n, uint32_t *ids,
+                                                       uint32_t *tokens_out, uint32_t *state, int count) {
+    int best_key = INT_MIN, best = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const int k = total_key(logits[i]);
+        if (k > best_key) {
+            best_key = k;
+            best = i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const int ok = __shfl_xor(best_key, o), oi = __shfl_xor(best, o);
+        if (ok > best_key || (ok == best_key && oi < best)) {
+            best_key = ok;
+            best = oi;
+        }
+    }
+    __shared__ int keys[16], idx[16];
+    if ((threadIdx.x & 63) == 0) {
+        keys[threadIdx.x >> 6] = best_key;
+        idx[threadIdx.x >> 6] = best;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int k = keys[0], b = idx[0];
+        for (int w = 1; w < 16; ++w)
+            if (keys[w] > k || (keys[w] == k && idx[w] < b)) {
+                k = keys[w];
+                b = idx[w];
+            }
+        ids[0] = (uint32_t)b;
+        if (tokens_out) tokens_out[state[2]] = (uint32_t)b;
+        state[0] += (uint32_t)count;
+        state[1] = state[0] + 1;
+        state[2] += 1;
+    }
+}
+
+// Sets the device state for a pass of `count` tokens at `pos`: pos, ctx = pos + count.
+__global__ void set_state(uint32_t *state, uint32_t pos, uint32_t count) {
+    state[0] = pos;
+    state[1] = pos + count;
+}
+
+__global__ void embed_device_ids(const uint8_t *__restrict__ codes, const float *__restrict__ scales,
+                                 const uint32_t *__restrict__ ids, float *__restrict__ out, int cols, int group) {
+    const size_t row = ids[blockIdx.x];
+    const int groups = cols / group;
+    const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
+    for (int i = threadIdx.x; i < cols; i += blockDim.x)
+        out[(size_t)blockIdx.x * cols + i] = (float)(int8_t)codes[row * cols + i] * srow[(i / group) * 16];
+}
+
+}  // namespace marin
+
+struct Layer {
+    marin_quant_matrix *qkv = nullptr, *o = nullptr, *gate_up = nullptr, *down = nullptr;
+    float *input_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+struct marin_qwen3 {
+    marin_gpu *gpu = nullptr;
+    marin_qwen3_config cfg{};
+    std::vector<Layer> layers;
+    marin_quant_matrix *embed = nullptr, *lm_head = nullptr;
+    float *final_norm = nullptr;
+    float *freq = nullptr;
+    size_t qd() const { return cfg.heads * cfg.head_dim; }
+    size_t kvd() const { return cfg.kv_heads * cfg.head_dim; }
+    const marin_quant_matrix *head() const { return lm_head ? lm_head : embed; }
+};
+
+struct marin_qwen3_cache {
+    marin_qwen3 *model = nullptr;
+    marin_kv *kv = nullptr;
+    // device workspace, CHUNK tokens
+    float *hidden = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr;
+    void *split_h = nullptr, *split_ctx = nullptr, *split_act = nullptr;
+    uint32_t *ids = nullptr, *state = nullptr, *tokens_out = nullptr;
+    size_t tokens_cap = 0;
+    float *attn_partials = nullptr;
+    size_t attn_partial_floats = 0;
+    hipGraphExec_t graph = nullptr;
+    size_t graph_capacity_ctx = 0;
+};
+
+static void check_config(const marin_qwen3_config *c) {
+    if (!c->layers || !c->hidden || !c->heads || !c->kv_heads || !c->head_dim || !c->ffn || !c->vocab)
+        shape("qwen3 config", 1, 0);
+    if (c->heads % c->kv_heads) shape("attention heads", c->kv_heads, c->heads);
+    if (c->head_dim > 256 || c->head_dim % 2) unsupported("head size (even)", 256, c->head_dim);
+    if (c->group == 0 || c->group % 64 || c->hidden % c->group || c->ffn % c->group ||
+        (c->heads * c->head_dim) % c->group)
+        shape("quantization group (a multiple of 64 dividing every width)", c->group, c->hidden);
+}
+
+static float *device_ones(marin_gpu *g, size_t n) {
+    std::vector<float> ones(n, 1.0f);
+    float *d = (float *)g->alloc(n * 4, false);
+    g->upload(d, ones.data(), n * 4);
+    return d;
+}
+
+static marin_qwen3 *alloc_model(marin_gpu *g, const marin_qwen3_config *cfg) {
+    check_config(cfg);
+    auto m = std::make_unique<marin_qwen3>();
+    m->gpu = g;
+    m->cfg = *cfg;
+    const size_t H = cfg->hidden, qd = cfg->heads * cfg->head_dim, kvd = cfg->kv_heads * cfg->head_dim;
+    m->layers.resize(cfg->layers);
+    try {
+        for (auto &L : m->layers) {
+            L.qkv = new_quant_matrix(g, qd + 2 * kvd, H, 8, cfg->group, false);
+            L.o = new_quant_matrix(g, H, qd, 8, cfg->group, false);
+            L.gate_up = new_quant_matrix(g, 2 * cfg->ffn, H, 8, cfg->group, false);
+            L.down = new_quant_matrix(g, H, cfg->ffn, 8, cfg->group, false);
+            L.input_norm = device_ones(g, H);
+            L.post_norm = device_ones(g, H);
+            L.q_norm = device_ones(g, cfg->head_dim);
+            L.k_norm = device_ones(g, cfg->head_dim);
+        }
+        m->embed = new_quant_matrix(g, cfg->vocab, H, 8, cfg->group, false);
+        if (!cfg->tie_embeddings) m->lm_head = new_quant_matrix(g, cfg->vocab, H, 8, cfg->group, false);
+        m->final_norm = device_ones(g, H);
+        m->freq = make_rope_frequencies(g, cfg->head_dim, cfg->rope_theta);
+    } catch (...) {
+        marin_qwen3_free(m.release());
+        throw;
+    }
+    return m.release();
+}
+
+// Where tensor `tensor` of a layer lands in the fused matrices: (matrix, first row, row step).
+static void placement(marin_qwen3 *m, int layer, int tensor, marin_quant_matrix *&mat, size_t &row0, size_t &step,
+                      size_t &rows, size_t &cols) {
+    const size_t H = m->cfg.hidden, qd = m->qd(), kvd = m->kvd(), F = m->cfg.ffn;
+    step = 1;
+    row0 = 0;
+    if (layer < 0) {
+        if (tensor == 0) mat = m->embed;
+        else if (tensor == 1 && m->lm_head) mat = m->lm_head;
+        else shape("model tensor", 1, (size_t)tensor);
+        rows = m->cfg.vocab;
+        cols = H;
+        return;
+    }
+    if ((size_t)layer >= m->layers.size()) shape("layer", m->layers.size(), (size_t)layer);
+    Layer &L = m->layers[layer];
+    switch (tensor) {
+        case 0: mat = L.qkv; rows = qd; cols = H; break;
+        case 1: mat = L.qkv; row0 = qd; rows = kvd; cols = H; break;
+        case 2: mat = L.qkv; row0 = qd + kvd; rows = kvd; cols = H; break;
+        case 3: mat = L.o; rows = H; cols = qd; break;
+        case 4: mat = L.gate_up; row0 = 0; step = 2; rows = F; cols = H; break;
+        case 5: mat = L.gate_up; row0 = 1; step = 2; rows = F; cols = H; break;
+        case 6: mat = L.down; rows = H; cols = F; break;
+        default: shape("layer tensor", 7, (size_t)tensor);
+    }
+}
+
+// Synthetic tensor streams (same numbering as oracle/qwen3_synth.c): embed 1, lm_head 2, layer l tensor i:
+// ((l + 1) << 8) | i.
+static uint64_t synth_stream(int layer, int tensor) {
+    if (layer < 0) return tensor == 0 ? 1u : 2u;
+    return ((uint64_t)(layer + 1) << 8) | (uint64_t)tensor;
+}
+
+static void free_cache_graph(marin_qwen3_cache *c) {
+    if (c->graph) {
+        (void)hipGraphExecDestroy(c->graph);
+        c->graph = nullptr;
+    }
+}
+
+// One pass over `n` (<= CHUNK) tokens whose ids are already in c->ids, at the position in c->state. Writes the last
+// token's logits. `max_ctx` bounds the context for the attention grid.
+static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx, size_t host_ctx = 0) {
+    marin_gpu *g = m->gpu;
+    const auto &cfg = m->cfg;
+    const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd(), F = cfg.ffn;
+    SplitView sh = split_view(c->split_h, n, H), sc = split_view(c->split_ctx, n, qd), sa = split_view(c->split_act, n, F);
+    embed_device_ids<<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(m->embed->codes, (const float *)m->embed->scales,
+                                                                      c->ids, c->hidden, (int)H, (int)cfg.group);
+    g->launched();
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        Layer &L = m->layers[l];
+        rms_norm_split_kernel<<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(c->hidden, L.input_norm, (int)H,
+                                                                              cfg.rms_eps, sh.data, sh.inv);
+        g->launched();
+        EpiArgs e;
+        e.y = c->qkv;
+        e.y_stride = qd + 2 * kvd;
+        launch_gemv_mfma(g, L.qkv, sh, n, EPI_F32, e);
+        const KvGeom geom = c->kv->geom(l);
+        dim3 grid((unsigned)n, (unsigned)(cfg.heads + 2 * cfg.kv_heads));
+#define MARIN_QK(F)                                                                                                 \
+    qk_norm_rope_store<F><<<grid, dim3(64), 0, g->stream>>>(c->qkv, c->q, L.q_norm, L.k_norm, m->freq,               \
+                                                          c->kv->page_ptrs, geom, c->state, (int)cfg.heads,          \
+                                                          (int)cfg.kv_heads, cfg.rms_eps)
+        if (c->kv->format == MARIN_KV_F32) MARIN_QK(MARIN_KV_F32);
+        else if (c->kv->format == MARIN_KV_F16) MARIN_QK(MARIN_KV_F16);
+        else MARIN_QK(MARIN_KV_BF16);
+#undef MARIN_QK
+        g->launched();
+        AttentionArgs a{};
+        a.q = c->q;
+        a.q_bf16 = false;
+        a.out = sc.data;
+        a.out_kind = 2;
+        a.split_inv = sc.inv;
+        a.tables = c->kv->page_ptrs;
+        a.table_stride = 0;
+        a.ctx = c->state + 1;
+        a.batch = 1;
+        a.tokens = n;
+        a.heads = cfg.heads;
+        a.kv_heads = cfg.kv_heads;
+        a.geom = geom;
+        a.max_ctx = max_ctx;
+        a.partials = c->attn_partials;
+        a.partial_floats = c->attn_partial_floats;
+        a.bytes_hint = (double)host_ctx * 2 * kvd * kv_elem_bytes(c->kv->format) + 2.0 * n * qd * 4;
+        launch_attention(g, a);
+        EpiArgs eo;
+        eo.y = c->hidden;
+        eo.y_stride = H;
+        launch_gemv_mfma(g, L.o, sc, n, EPI_ADD, eo);
+        rms_norm_split_kernel<<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(c->hidden, L.post_norm, (int)H,
+                                                                              cfg.rms_eps, sh.data, sh.inv);
+        g->launched();
+        EpiArgs eg;
+        eg.split_out = sa;
+        launch_gemv_mfma(g, L.gate_up, sh, n, EPI_SILU_SPLIT, eg);
+        EpiArgs ed;
+        ed.y = c->hidden;
+        ed.y_stride = H;
+        launch_gemv_mfma(g, L.down, sa, n, EPI_ADD, ed);
+    }
+    SplitView last = split_view(c->split_h, 1, H);
+    rms_norm_split_kernel<<<dim3(1), dim3(256), 0, g->stream>>>(c->hidden + (n - 1) * H, m->final_norm, (int)H,
+                                                                cfg.rms_eps, last.data, last.inv);
+    g->launched();
+    EpiArgs el;
+    el.y = c->logits;
+    el.y_stride = cfg.vocab;
+    launch_gemv_mfma(g, m->head(), last, 1, EPI_F32, el);
+}
+
+static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n) {
+    marin_gpu *g = m->gpu;
+    const size_t start = c->kv->len;
+    if (n == 0) throw Error(MARIN_SHAPE, "no tokens", 1, 0);
+    if (start + n > c->kv->capacity) shape("kv positions", c->kv->capacity, start + n);
+    for (size_t i = 0; i < n; ++i)
+        if (ids[i] >= m->cfg.vocab) shape("token id", m->cfg.vocab, ids[i]);
+    c->kv->reserve(start + n);
+    for (size_t t0 = 0; t0 < n; t0 += CHUNK) {
+        const size_t nt = std::min(CHUNK, n - t0);
+        void *staged = g->stage(ids + t0, nt * 4);
+        HIP_CHECK(hipMemcpyAsync(c->ids, staged, nt * 4, hipMemcpyHostToDevice, g->stream));
+        set_state<<<1, 1, 0, g->stream>>>(c->state, (uint32_t)(start + t0), (uint32_t)nt);
+        g->launched();
+        pass(m, c, nt, start + t0 + nt);
+        c->kv->len = start + t0 + nt;
+    }
+}
+
+extern "C" {
+
+marin_status marin_qwen3_new_empty(marin_gpu *g, const marin_qwen3_config *cfg, marin_qwen3 **out) {
+    return guard([&] { *out = alloc_model(g, cfg); });
+}
+
+marin_status marin_qwen3_new_synthetic(marin_gpu *g, const marin_qwen3_config *cfg, uint64_t seed, marin_qwen3 **out) {
+    return guard([&] {
+        marin_qwen3 *m = alloc_model(g, cfg);
+        try {
+            for (int l = -1; l < (int)cfg->layers; ++l) {
+                const int tensors = l < 0 ? (cfg->tie_embeddings ? 1 : 2) : 7;
+                for (int t = 0; t < tensors; ++t) {
+                    marin_quant_matrix *mat;
+                    size_t row0, step, rows, cols;
+                    placement(m, l, t, mat, row0, step, rows, cols);
+                    launch_synth_quantize(g, mat, seed, synth_stream(l, t), 0.02, rows, row0, step);
+                }
+            }
+            HIP_CHECK(hipStreamSynchronize(g->stream));
+        } catch (...) {
+            marin_qwen3_free(m);
+            throw;
+        }
+        *out = m;
+    });
+}
+
+marin_status marin_qwen3_load_matrix(marin_qwen3 *m, int layer, int tensor, size_t rows, size_t cols,
+                                     const uint8_t *codes, const float *scales) {
+    return guard([&] {
+        marin_quant_matrix *mat;
+        size_t row0, step, r, c;
+        placement(m, layer, tensor, mat, row0, step, r, c);
+        if (rows != r || cols != c) shape("tensor rows", r, rows);
+        upload_rows(mat, codes, scales, rows, row0, step);
+    });
+}
+
+marin_status marin_qwen3_load_vector(marin_qwen3 *m, int layer, int which, const float *values, size_t len) {
+    return guard([&] {
+        float *dst = nullptr;
+        size_t want = m->cfg.hidden;
+        if (layer < 0) {
+            if (which != 0) shape("model vector", 1, (size_t)which);
+            dst = m->final_norm;
+        } else {
+            if ((size_t)layer >= m->layers.size()) shape("layer", m->layers.size(), (size_t)layer);
+            Layer &L = m->layers[layer];
+            switch (which) {
+                case 0: dst = L.input_norm; break;
+                case 1: dst = L.post_norm; break;
+                case 2: dst = L.q_norm; want = m->cfg.head_dim; break;
+                case 3: dst = L.k_norm; want = m->cfg.head_dim; break;
+                default: shape("layer vector", 4, (size_t)which);
+            }
+        }
+        check_len("vector length", want, len);
+        m->gpu->upload(dst, values, len * 4);
+    });
+}
+
+void marin_qwen3_free(marin_qwen3 *m) {
+    if (!m) return;
+    marin_gpu *g = m->gpu;
+    (void)hipStreamSynchronize(g->stream);
+    for (auto &L : m->layers) {
+        free_quant_matrix(L.qkv);
+        free_quant_matrix(L.o);
+        free_quant_matrix(L.gate_up);
+        free_quant_matrix(L.down);
+        g->release(L.input_norm);
+        g->release(L.post_norm);
+        g->release(L.q_norm);
+        g->release(L.k_norm);
+    }
+    free_quant_matrix(m->embed);
+    free_quant_matrix(m->lm_head);
+    g->release(m->final_norm);
+    g->release(m->freq);
+    delete m;
+}
+
+marin_status marin_qwen3_cache_new(marin_qwen3 *m, size_t capacity, marin_kv_format format, marin_qwen3_cache **out) {
+    return guard([&] {
+        marin_gpu *g = m->gpu;
+        const auto &cfg = m->cfg;
+        auto c = std::make_unique<marin_qwen3_cache>();
+        c->model = m;
+        marin_status s = marin_kv_new(g, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, capacity, format, &c->kv);
+        if (s != MARIN_OK) throw Error(s, marin_last_error());
+        try {
+            const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd();
+            c->hidden = (float *)g->alloc(CHUNK * H * 4, true);
+            c->qkv = (float *)g->alloc(CHUNK * (qd + 2 * kvd) * 4, true);
+            c->q = (float *)g->alloc(CHUNK * qd * 4, true);
+            c->logits = (float *)g->alloc(cfg.vocab * 4, true);
+            c->split_h = g->alloc(split_bytes(CHUNK, H), true);
+            c->split_ctx = g->alloc(split_bytes(CHUNK, qd), true);
+            c->split_act = g->alloc(split_bytes(CHUNK, cfg.ffn), true);
+            c->ids = (uint32_t *)g->alloc(CHUNK * 4, true);
+            c->state = (uint32_t *)g->alloc(16, true);
+            c->attn_partial_floats = attention_partial_floats(1, CHUNK, cfg.heads, cfg.head_dim, capacity, g->cu_count);
+            c->attn_partials = (float *)g->alloc(c->attn_partial_floats * 4, false);
+            // The GEMV cross-block scratch for every shape this model uses, sized now so no pass allocates.
+            size_t most_rows = std::max({m->layers[0].qkv->rows_padded, m->layers[0].gate_up->rows_padded,
+                                         m->head()->rows_padded});
+            g->ensure_partials(64 * CHUNK * most_rows, most_rows / 16 + 1);
+        } catch (...) {
+            marin_qwen3_cache_free(c.release());
+            throw;
+        }
+        *out = c.release();
+    });
+}
+
+void marin_qwen3_cache_free(marin_qwen3_cache *c) {
+    if (!c) return;
+    marin_gpu *g = c->model->gpu;
+    (void)hipStreamSynchronize(g->stream);
+    free_cache_graph(c);
+    marin_kv_free(c->kv);
+    for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->q, (void *)c->logits, c->split_h, c->split_ctx,
+                    c->split_act, (void *)c->ids, (void *)c->state, (void *)c->attn_partials, (void *)c->tokens_out})
+        g->release(p);
+    delete c;
+}
+
+size_t marin_qwen3_cache_len(const marin_qwen3_cache *c) { return c->kv->len; }
+
+marin_status marin_qwen3_cache_truncate(marin_qwen3_cache *c, size_t len) { return marin_kv_truncate(c->kv, len); }
+
+marin_status marin_qwen3_forward(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n, float *logits) {
+    return guard([&] {
+        run_prompt(m, c, ids, n);
+        m->gpu->download(logits, c->logits, m->cfg.vocab * 4);
+    });
+}
+
+// One decode step on the device: choose the next token from the last pass's logits, then run it through the model.
+static void decode_step(marin_qwen3 *m, marin_qwen3_cache *c, size_t host_ctx) {
+    marin_gpu *g = m->gpu;
+    argmax_advance<<<1, 1024, 0, g->stream>>>(c->logits, (int)m->cfg.vocab, c->ids, c->tokens_out, c->state, 1);
+    g->launched();
+    pass(m, c, 1, c->kv->capacity, host_ctx);
+}
+
+static bool graphs_enabled() {
+    const char *v = getenv("MARIN_NO_GRAPH");
+    return !(v && *v && *v != '0');
+}
+
+// Greedy decoding of `steps` tokens from the cache's last logits; each chosen token is fed through the model, so the
+// cache then holds the logits after the last one. The per-step launches are captured once into a HIP graph.
+static void decode(marin_qwen3 *m, marin_qwen3_cache *c, size_t steps, uint32_t *tokens_out) {
+    marin_gpu *g = m->gpu;
+    if (steps == 0) return;
+    const size_t len = c->kv->len;
+    if (len == 0) throw Error(MARIN_SHAPE, "decode needs a forward pass first", 1, 0);
+    if (len + steps > c->kv->capacity) shape("kv positions", c->kv->capacity, len + steps);
+    c->kv->reserve(len + steps);
+    if (steps > c->tokens_cap) {
+        HIP_CHECK(hipStreamSynchronize(g->stream));
+        free_cache_graph(c);  // the graph holds the old tokens_out address
+        g->release(c->tokens_out);
+        c->tokens_out = nullptr;
+        c->tokens_out = (uint32_t *)g->alloc(steps * 4, false);
+        c->tokens_cap = steps;
+    }
+    // state: pos = len - 1 (advanced to len by the first choice), ctx = len, step 0
+    const uint32_t init[3] = {(uint32_t)(len - 1), (uint32_t)len, 0u};
+    void *staged = g->stage(init, sizeof(init));
+    HIP_CHECK(hipMemcpyAsync(c->state, staged, sizeof(init), hipMemcpyHostToDevice, g->stream));
+    if (graphs_enabled()) {
+        if (!c->graph) {
+            hipGraph_t graph;
+            HIP_CHECK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
+            try {
+                decode_step(m, c, 0);
+            } catch (...) {
+                hipGraph_t junk;
+                (void)hipStreamEndCapture(g->stream, &junk);
+                if (junk) (void)hipGraphDestroy(junk);
+                throw;
+            }
+            HIP_CHECK(hipStreamEndCapture(g->stream, &graph));
+            hipError_t e = hipGraphInstantiate(&c->graph, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            hip_check(e, "hipGraphInstantiate");
+        }
+        for (size_t s = 0; s < steps; ++s) {
+            HIP_CHECK(hipGraphLaunch(c->graph, g->stream));
+            g->traffic.launches++;
+        }
+    } else {
+        for (size_t s = 0; s < steps; ++s) decode_step(m, c, 0);
+    }
+    c->kv->len = len + steps;
+    if (tokens_out) g->download(tokens_out, c->tokens_out, steps * 4);
+}
+
+marin_status marin_qwen3_generate(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *prompt, size_t n,
+                                  size_t steps, uint32_t *tokens_out) {
+    return guard([&] {
+        if (c->kv->len + n + steps > c->kv->capacity) shape("kv positions", c->kv->capacity, c->kv->len + n + steps);
+        run_prompt(m, c, prompt, n);
+        decode(m, c, steps, tokens_out);
+    });
+}
+
+marin_status marin_qwen3_decode(marin_qwen3 *m, marin_qwen3_cache *c, size_t steps, uint32_t *tokens_out) {
+    return guard([&] { decode(m, c, steps, tokens_out); });
+}
+
+marin_status marin_qwen3_profile_step(marin_qwen3 *m, marin_qwen3_cache *c, marin_step_profile *out) {
+    return guard([&] {
+        marin_gpu *g = m->gpu;
+        const size_t len = c->kv->len;
+        if (len == 0) throw Error(MARIN_SHAPE, "decode needs a forward pass first", 1, 0);
+        if (len + 1 > c->kv->capacity) shape("kv positions", c->kv->capacity, len + 1);
+        c->kv->reserve(len + 1);
+        if (!c->tokens_out) {
+            c->tokens_out = (uint32_t *)g->alloc(4, false);
+            c->tokens_cap = 1;
+        }
+        const uint32_t init[3] = {(uint32_t)(len - 1), (uint32_t)len, 0u};
+        void *staged = g->stage(init, sizeof(init));
+        HIP_CHECK(hipMemcpyAsync(c->state, staged, sizeof(init), hipMemcpyHostToDevice, g->stream));
+        std::vector<marin_gpu::ProfileEntry> entries;
+        entries.reserve(1024);
+        hipEvent_t start;
+        HIP_CHECK(hipEventCreate(&start));
+        HIP_CHECK(hipEventRecord(start, g->stream));
+        g->profile = &entries;
+        try {
+            decode_step(m, c, len + 1);
+        } catch (...) {
+            g->profile = nullptr;
+            (void)hipEventDestroy(start);
+            throw;
+        }
+        g->profile = nullptr;
+        HIP_CHECK(hipStreamSynchronize(g->stream));
+        marin_step_profile p{};
+        hipEvent_t prev = start;
+        for (auto &e : entries) {
+            float ms = 0.0f;
+            HIP_CHECK(hipEventElapsedTime(&ms, prev, e.event));
+            const double s = ms * 1e-3;
+            if (e.kind == marin_gpu::GEMV) {
+                p.gemv_seconds += s;
+                p.gemv_bytes += e.bytes;
+                p.gemv_launches++;
+            } else if (e.kind == marin_gpu::ATTENTION) {
+                p.attention_seconds += s;
+                p.attention_bytes += e.bytes;
+                p.attention_launches++;
+            } else {
+                p.other_seconds += s;
+                p.other_launches++;
+            }
+            p.step_seconds += s;
+            prev = e.event;
+        }
+        (void)hipEventDestroy(start);
+        c->kv->len = len + 1;
+        *out = p;
+    });
+}
+
+}  // extern "C"

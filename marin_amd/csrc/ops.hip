@@ -67,6 +67,14 @@ const float *rope_frequencies(marin_gpu *g, size_t hd, float theta) {
     return d;
 }
 
+float *make_rope_frequencies(marin_gpu *g, size_t hd, float theta) {
+    std::vector<float> f(hd / 2);
+    for (size_t i = 0; i < hd / 2; ++i) f[i] = powf(theta, -((float)i * 2.0f / (float)hd));
+    float *d = (float *)g->alloc(std::max<size_t>(f.size(), 1) * 4, false);
+    g->upload(d, f.data(), f.size() * 4);
+    return d;
+}
+
 void forget_rope_frequencies(marin_gpu *g) {
     std::lock_guard<std::mutex> lock(g_freq_mutex);
     for (auto it = g_freq.begin(); it != g_freq.end();) {

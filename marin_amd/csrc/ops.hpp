@@ -10,5 +10,7 @@ void launch_rope(marin_gpu *g, float *x, size_t head_count, size_t heads, size_t
 // theta^(-2i/hd) for i < hd/2, computed on the host with powf and cached on the device per (gpu, hd, theta).
 const float *rope_frequencies(marin_gpu *g, size_t hd, float theta);
 void forget_rope_frequencies(marin_gpu *g);
+// The same table in memory the caller owns (released with gpu->release).
+float *make_rope_frequencies(marin_gpu *g, size_t hd, float theta);
 
 }  // namespace marin

@@ -141,12 +141,14 @@ constexpr int MAX_COLS = 16;  // B columns of one MFMA
 // Grid: x = row blocks, y = column splits (kb). With more than one split, each block leaves its sums in `partials`
 // and the last block to arrive at a row block's counter adds them in split order, so results do not depend on
 // timing; that block also puts the counter back to zero.
-template <int RT, typename ST, int EPI, int PARTS>
+template <int RT, typename ST, int EPI, int PARTS, bool ONE>
 __global__ __launch_bounds__(256) void gemv_i8_mfma(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                    const _Float16 *__restrict__ xs, const float *__restrict__ xinv,
-                                                   int tokens, int rows, int rows_padded, int cols, int group,
+                                                   int tokens_arg, int rows, int rows_padded, int cols, int group,
                                                    int windows_per_split, float *__restrict__ partials,
                                                    unsigned *__restrict__ counters, EpiArgs epi) {
+    // ONE: a single token (decode), known at compile time; otherwise up to MAX_GEMV_TOKENS.
+    const int tokens = ONE ? 1 : tokens_arg;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, q = lane >> 4;
     const int used = tokens * PARTS;
@@ -328,15 +330,24 @@ static void launch_mfma_t(marin_gpu *g, const marin_quant_matrix *w, SplitView x
     if (splits > 1) g->ensure_partials((size_t)splits * tokens * w->rows_padded, blocks_x);
     const ST *sc = (const ST *)w->scales;
     dim3 grid((unsigned)blocks_x, (unsigned)splits);
-#define MARIN_LAUNCH(RT)                                                                                         \
-    gemv_i8_mfma<RT, ST, EPI, PARTS><<<grid, dim3(256), 0, g->stream>>>(                                        \
+#define MARIN_LAUNCH1(RT, ONE)                                                                                   \
+    gemv_i8_mfma<RT, ST, EPI, PARTS, ONE><<<grid, dim3(256), 0, g->stream>>>(                                   \
         w->codes, sc, x.data, x.inv, (int)tokens, (int)w->rows, (int)w->rows_padded, (int)w->cols, (int)w->group, \
         per_split, g->partials, g->counters, args)
+#define MARIN_LAUNCH(RT)                    \
+    do {                                    \
+        if (tokens == 1) MARIN_LAUNCH1(RT, true); \
+        else MARIN_LAUNCH1(RT, false);      \
+    } while (0)
     if (rt == 4) MARIN_LAUNCH(4);
     else if (rt == 2) MARIN_LAUNCH(2);
     else MARIN_LAUNCH(1);
 #undef MARIN_LAUNCH
-    g->launched();
+#undef MARIN_LAUNCH1
+    // algorithmic bytes: codes + scales once, activations (f32) and outputs once
+    const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * w->groups() * (w->bf16_scales ? 2 : 4) +
+                         (double)tokens * w->cols * 4 + (double)tokens * w->rows * 4;
+    g->launched(marin_gpu::GEMV, bytes);
 }
 
 template <int EPI, int PARTS>
@@ -657,6 +668,22 @@ static void check_quantized(size_t rows, size_t cols, int bits, size_t group, si
 }
 
 extern "C" {
+
+marin_status marin_quantized_synthetic(marin_gpu *g, size_t rows, size_t cols, size_t group, uint64_t seed,
+                                       uint64_t stream, double std_dev, marin_quant_matrix **out) {
+    return guard([&] {
+        if (group == 0 || group % 32 != 0 || cols % group != 0) shape("quantization group", group, cols);
+        if (!rows) shape("rows", 1, 0);
+        marin_quant_matrix *m = new_quant_matrix(g, rows, cols, 8, group, false);
+        try {
+            launch_synth_quantize(g, m, seed, stream, std_dev, rows, 0, 1);
+        } catch (...) {
+            free_quant_matrix(m);
+            throw;
+        }
+        *out = m;
+    });
+}
 
 marin_status marin_upload_quantized(marin_gpu *g, size_t rows, size_t cols, int bits, size_t group,
                                     const uint8_t *codes, size_t codes_len, const float *scales, size_t scales_len,

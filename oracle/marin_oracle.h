@@ -137,9 +137,10 @@ void *or_qwen3_synth_new(const or_synth_config *cfg);
 or_qwen3 *or_qwen3_synth_model(void *handle);
 void or_qwen3_synth_free(void *handle);
 /* Prompt pass then `steps` greedy tokens. tokens_out[steps]; gaps_out[steps] = top-1 minus top-2 logit of each step
- * (how far the choice is from a tie). Returns 0 on success. */
+ * (how far the choice is from a tie); top_ids/top_vals[steps * 5] (optional) the five best logits of each step.
+ * Returns 0 on success. */
 int or_qwen3_greedy(void *handle, const uint32_t *prompt, size_t prompt_len, size_t steps, uint32_t *tokens_out,
-                    float *gaps_out, size_t prefill_chunk);
+                    float *gaps_out, size_t prefill_chunk, uint32_t *top_ids, float *top_vals);
 
 #ifdef __cplusplus
 }

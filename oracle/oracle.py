@@ -313,14 +313,16 @@ lib.or_qwen3_synth_new.restype = C.c_void_p
 lib.or_qwen3_synth_new.argtypes = [C.c_void_p]
 lib.or_qwen3_synth_free.argtypes = [C.c_void_p]
 lib.or_qwen3_greedy.restype = C.c_int
-lib.or_qwen3_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_size_t]
+lib.or_qwen3_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_size_t,
+                                C.c_void_p, C.c_void_p]
 
 
 def synth_prompt(seed: int, length: int, vocab: int) -> np.ndarray:
     return np.array([lib.or_synth_prompt(seed, i, vocab) for i in range(length)], np.uint32)
 
 
-def synth_greedy(shape: dict, seed: int, prompt, steps: int, kv_f16: bool = False, prefill_chunk: int = 0):
+def synth_greedy(shape: dict, seed: int, prompt, steps: int, kv_f16: bool = False, prefill_chunk: int = 0,
+                 with_top: bool = False):
     """Greedy tokens and top-1/top-2 gaps of the synthetic model ``shape`` (keys as in marin_amd.qwen3.SHAPES)."""
     prompt = np.ascontiguousarray(prompt, np.uint32)
     cfg = _SynthConfig(layers=shape["layers"], hidden=shape["hidden"], heads=shape["heads"],
@@ -334,10 +336,14 @@ def synth_greedy(shape: dict, seed: int, prompt, steps: int, kv_f16: bool = Fals
     try:
         toks = np.zeros(steps, np.uint32)
         gaps = np.zeros(steps, np.float32)
+        top_ids = np.zeros(steps * 5, np.uint32)
+        top_vals = np.zeros(steps * 5, np.float32)
         rc = lib.or_qwen3_greedy(h, prompt.ctypes.data, prompt.size, steps, toks.ctypes.data, gaps.ctypes.data,
-                                 prefill_chunk)
+                                 prefill_chunk, top_ids.ctypes.data, top_vals.ctypes.data)
         if rc:
             raise ValueError(f"oracle generation failed ({rc})")
+        if with_top:
+            return toks, gaps, top_ids.reshape(steps, 5), top_vals.reshape(steps, 5)
         return toks, gaps
     finally:
         lib.or_qwen3_synth_free(h)

@@ -49,7 +49,16 @@ static int make_matrix(synth *s, uint64_t seed, uint64_t stream, size_t rows, si
     or_synth_fill(seed, stream, 0.02, bits, rows * cols);
     uint8_t *codes = (uint8_t *)own(s, rows * cols);
     float *scales = (float *)own(s, rows * (cols / group) * sizeof(float));
-    long rc = or_quantize(bits, rows, cols, 8, group, codes, scales);
+    /* Rows are quantized independently (tensor/src/quant.rs:134-170 splits them across threads the same way). */
+    int bad = 0;
+#pragma omp parallel for schedule(static) reduction(| : bad)
+    for (long r0 = 0; r0 < (long)rows; r0 += 256) {
+        size_t n = rows - (size_t)r0 < 256 ? rows - (size_t)r0 : 256;
+        if (or_quantize(bits + (size_t)r0 * cols, n, cols, 8, group, codes + (size_t)r0 * cols,
+                        scales + (size_t)r0 * (cols / group)) != -1)
+            bad = 1;
+    }
+    long rc = bad ? 0 : -1;
     free(bits);
     m->rows = rows;
     m->cols = cols;
@@ -115,7 +124,7 @@ void or_qwen3_synth_free(void *handle) {
 }
 
 int or_qwen3_greedy(void *handle, const uint32_t *prompt, size_t prompt_len, size_t steps, uint32_t *tokens_out,
-                    float *gaps_out, size_t prefill_chunk) {
+                    float *gaps_out, size_t prefill_chunk, uint32_t *top_ids, float *top_vals) {
     or_qwen3 *M = &((synth *)handle)->model;
     float *logits = (float *)malloc(M->vocab * sizeof(float));
     if (prefill_chunk == 0) prefill_chunk = prompt_len;
@@ -131,6 +140,20 @@ int or_qwen3_greedy(void *handle, const uint32_t *prompt, size_t prompt_len, siz
             if (i != best && logits[i] > second) second = logits[i];
         tokens_out[s] = best;
         if (gaps_out) gaps_out[s] = logits[best] - second;
+        if (top_ids) { /* the five largest, ties to the lower id */
+            for (int k = 0; k < 5; ++k) {
+                uint32_t pick = 0;
+                int found = 0;
+                for (size_t i = 0; i < M->vocab; ++i) {
+                    int taken = 0;
+                    for (int j = 0; j < k; ++j) taken |= top_ids[s * 5 + j] == i;
+                    if (taken) continue;
+                    if (!found || logits[i] > logits[pick]) { pick = (uint32_t)i; found = 1; }
+                }
+                top_ids[s * 5 + k] = pick;
+                top_vals[s * 5 + k] = logits[pick];
+            }
+        }
         if (s + 1 < steps) rc = or_qwen3_forward(M, &best, 1, logits);
     }
     free(logits);

@@ -1,0 +1,139 @@
+"""End-to-end parity of the Qwen3 decode driver on the GPU against the CPU oracle.
+
+- synthetic weights: generated and quantized on the device, bit-exact with the oracle's generator + quantizer;
+- tiny-qwen3 (the reference's HF fixture) quantized int8 g64: logits against the oracle's forward on the same codes;
+- synthetic Qwen3-shaped models: greedy tokens equal to the committed oracle goldens (tests/golden/qwen3_*.json),
+  through the HIP-graph decode loop and the eager one, and per-step top-5 logits within tolerance;
+- model/tests/quantized.rs: a one-token pass equals a prompt pass within 1e-3, runs repeat exactly, and a decode
+  step allocates nothing.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import marin_amd as m
+from marin_amd.qwen3 import Qwen3
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def golden(name):
+    path = os.path.join(GOLDEN, f"qwen3_{name}_greedy.json")
+    if not os.path.exists(path):
+        pytest.skip(f"{path} not generated (tests/golden/make_qwen3_golden.py {name})")
+    return json.load(open(path))
+
+
+@pytest.mark.parametrize("rows,cols,group,seed,stream", [(300, 512, 128, 5, 77), (64, 4096, 64, 9, 3),
+                                                         (130, 768, 256, 1, 1 << 8)])
+def test_device_synthetic_weights_and_quantizer_are_bit_exact(gpu, rows, cols, group, seed, stream):
+    w = gpu.quantized_synthetic(rows, cols, group, seed, stream)
+    ids = gpu.tokens(rows)
+    out = gpu.zeros(rows * cols)
+    gpu.embed_quant(w, np.arange(rows), ids, out)
+    codes, scales = o.quantize(o.synth(seed, stream, rows * cols), rows, cols, 8, group)
+    expected = o.dequantize(codes, scales, rows, cols, 8, group).ravel()
+    assert np.array_equal(gpu.download(out).view(np.uint32), expected.view(np.uint32))
+
+
+def tiny():
+    d = os.path.join(GOLDEN, "tiny-qwen3")
+    cfg = json.load(open(os.path.join(d, "config.json")))
+    w = o.load_safetensors_f32(os.path.join(d, "model.safetensors"))
+    ref = json.load(open(os.path.join(d, "reference.json")))
+    return cfg, w, ref
+
+
+@pytest.mark.parametrize("fmt", [m.KvFormat.F32, m.KvFormat.F16])
+def test_tiny_qwen3_int8_matches_the_oracle_on_the_same_codes(gpu, fmt):
+    cfg, w, ref = tiny()
+    model = Qwen3.from_hf(gpu, cfg, w, o.quantize, group=64)
+    for case in ref["cases"]:
+        cache = model.new_cache(128, fmt)
+        oracle = o.Qwen3Oracle(cfg, w, 128, group=64, kv_f16=fmt == m.KvFormat.F16)
+        got = model.forward(case["prompt_ids"], cache)
+        exp = oracle.forward(case["prompt_ids"])
+        # f16 storage: a last-bit difference in a key before rounding can move it by one f16 ulp (2^-11)
+        tol = 1e-4 if fmt == m.KvFormat.F32 else 2.0 ** -11 * 4
+        for step in case["steps"]:
+            assert np.abs(got - exp).max() <= tol * (1 + np.abs(exp).max())
+            assert o.argmax(got) == o.argmax(exp)
+            got = model.forward([step["token"]], cache)
+            exp = oracle.forward([step["token"]])
+
+
+@pytest.mark.parametrize("name", ["mini", "mini_f16kv", "mini_tied"])
+def test_synthetic_greedy_tokens_match_the_golden(gpu, name, monkeypatch):
+    g = golden(name)
+    fmt = m.KvFormat.F16 if g["kv_f16"] else m.KvFormat.F32
+    model = Qwen3(gpu, g["shape"], seed=g["seed"])
+    steps = len(g["tokens"])
+    for graph in (True, False):
+        monkeypatch.setenv("MARIN_NO_GRAPH", "0" if graph else "1")
+        cache = model.new_cache(len(g["prompt"]) + steps + 1, fmt)
+        toks = model.generate(g["prompt"], steps, cache)
+        assert toks.tolist() == g["tokens"], f"graph={graph}"
+    # step-by-step logits against the oracle's top five
+    cache = model.new_cache(len(g["prompt"]) + steps + 1, fmt)
+    logits = model.forward(g["prompt"], cache)
+    for s in range(steps):
+        ids, vals = g["top_ids"][s], np.array(g["top_vals"][s])
+        assert np.abs(logits[ids] - vals).max() <= 1e-3 * (1 + np.abs(vals).max()), s
+        assert o.argmax(logits) == g["tokens"][s]
+        logits = model.forward([g["tokens"][s]], cache)
+
+
+def test_one_token_pass_equals_a_prompt_pass_and_runs_repeat(gpu):  # model/tests/quantized.rs:74-97
+    g = golden("mini")
+    model = Qwen3(gpu, g["shape"], seed=g["seed"])
+    prompt = g["prompt"][:20]
+    whole = model.forward(prompt + [3, 5], model.new_cache(64))
+    c = model.new_cache(64)
+    model.forward(prompt, c)
+    model.forward([3], c)
+    step = model.forward([5], c)
+    assert np.abs(whole - step).max() < 1e-3
+    again = model.forward(prompt + [3, 5], model.new_cache(64))
+    assert np.array_equal(whole, again)
+
+
+def test_a_decode_step_allocates_nothing(gpu):  # model/tests/quantized.rs:98-118
+    g = golden("mini")
+    model = Qwen3(gpu, g["shape"], seed=g["seed"])
+    c = model.new_cache(128)
+    model.forward(g["prompt"], c)
+    model.decode(2, c)
+    before = gpu.traffic().allocations
+    model.forward([7], c)
+    model.decode(8, c)
+    assert gpu.traffic().allocations == before
+
+
+@pytest.mark.parametrize("name", ["1.7b", "8b"])
+def test_model_shaped_greedy_tokens_match_the_golden(gpu, name):
+    g = golden(name)
+    model = Qwen3(gpu, g["shape"], seed=g["seed"])
+    steps = len(g["tokens"])
+    cache = model.new_cache(len(g["prompt"]) + steps + 1)
+    toks = model.generate(g["prompt"], steps, cache)
+    assert toks.tolist() == g["tokens"]
+    cache = model.new_cache(len(g["prompt"]) + 2)
+    logits = model.forward(g["prompt"], cache)
+    ids, vals = g["top_ids"][0], np.array(g["top_vals"][0])
+    assert np.abs(logits[ids] - vals).max() <= 1e-3 * (1 + np.abs(vals).max())
+
+
+def test_profiled_step_accounts_every_launch(gpu):
+    g = golden("mini")
+    model = Qwen3(gpu, g["shape"], seed=g["seed"])
+    c = model.new_cache(128)
+    model.forward(g["prompt"], c)
+    p = model.profile_step(c)
+    L = g["shape"]["layers"]
+    assert p["gemv_launches"] == 4 * L + 1
+    assert p["attention_launches"] == 2 * L
+    assert p["gemv_bytes"] > 0 and p["gemv_seconds"] > 0 and p["step_seconds"] >= p["gemv_seconds"]
