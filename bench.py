@@ -80,7 +80,11 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the decode step's kernels one by one instead of replaying a HIP graph (for tracers)")
     args = ap.parse_args()
+    if args.no_graph:
+        os.environ["MARIN_NO_GRAPH"] = "1"
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the one-GPU throughput is the reported value", file=sys.stderr)

@@ -84,6 +84,11 @@ marin_status guard(F &&f) {
 
 size_t dtype_bytes(marin_dtype d);
 
+// Instantiated HIP graphs still alive at process exit are destroyed by an atexit handler that runs before the HIP
+// runtime's own teardown.
+void register_graph(hipGraphExec_t g);
+void unregister_graph(hipGraphExec_t g);
+
 }  // namespace marin
 
 // Device memory with the context that owns it.
@@ -108,14 +113,6 @@ struct marin_gpu {
     std::string name, arch;
     // Counters of crates/cuda/src/counters.rs:10-89.
     marin_traffic traffic{};
-    // Workspace the quantized products use: the f16 split of the activations and the cross-block partial sums with
-    // their arrival counters (counters return to zero after every product, so they are cleared only once).
-    void *split = nullptr;
-    size_t split_bytes = 0;
-    float *partials = nullptr;
-    size_t partial_floats = 0;
-    unsigned *counters = nullptr;
-    size_t counter_count = 0;
     // Pinned staging for small host->device copies (token ids, page addresses).
     void *pinned = nullptr;
     size_t pinned_bytes = 0;
@@ -130,8 +127,6 @@ struct marin_gpu {
     void destroy();
     void upload(void *dst, const void *src, size_t bytes);  // synchronous with respect to the host data
     void download(void *dst, const void *src, size_t bytes);
-    void ensure_split(size_t bytes);
-    void ensure_partials(size_t floats, size_t counters);
     void *stage(const void *src, size_t bytes);  // copies into pinned memory; valid until the next stage()
 
     // Launch accounting. With a profile attached, every launch records an event after itself, tagged with its kind

@@ -3,6 +3,8 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
+#include <set>
 
 #include "common.hpp"
 #include "ops.hpp"
@@ -38,6 +40,28 @@ size_t dtype_bytes(marin_dtype d) {
         case MARIN_U8: return 1;
     }
     return 4;
+}
+
+static std::mutex g_graph_mutex;
+static std::set<hipGraphExec_t> *g_graphs = nullptr;
+
+void register_graph(hipGraphExec_t g) {
+    std::lock_guard<std::mutex> lock(g_graph_mutex);
+    if (!g_graphs) g_graphs = new std::set<hipGraphExec_t>();
+    g_graphs->insert(g);
+}
+
+void unregister_graph(hipGraphExec_t g) {
+    std::lock_guard<std::mutex> lock(g_graph_mutex);
+    if (g_graphs) g_graphs->erase(g);
+}
+
+static void destroy_graphs_at_exit() {
+    std::lock_guard<std::mutex> lock(g_graph_mutex);
+    if (!g_graphs) return;
+    (void)hipDeviceSynchronize();
+    for (hipGraphExec_t g : *g_graphs) (void)hipGraphExecDestroy(g);
+    g_graphs->clear();
 }
 
 }  // namespace marin
@@ -87,35 +111,6 @@ void marin_gpu::download(void *dst, const void *src, size_t bytes) {
     HIP_CHECK(hipStreamSynchronize(stream));
     traffic.downloads++;
     traffic.download_bytes += bytes;
-}
-
-void marin_gpu::ensure_split(size_t bytes) {
-    if (bytes <= split_bytes) return;
-    HIP_CHECK(hipStreamSynchronize(stream));
-    release(split);
-    split = nullptr;
-    split_bytes = 0;
-    split = alloc(bytes, true);
-    split_bytes = bytes;
-}
-
-void marin_gpu::ensure_partials(size_t floats, size_t count) {
-    if (floats > partial_floats) {
-        HIP_CHECK(hipStreamSynchronize(stream));
-        release(partials);
-        partials = nullptr;
-        partial_floats = 0;
-        partials = (float *)alloc(floats * 4, false);
-        partial_floats = floats;
-    }
-    if (count > counter_count) {
-        HIP_CHECK(hipStreamSynchronize(stream));
-        release(counters);
-        counters = nullptr;
-        counter_count = 0;
-        counters = (unsigned *)alloc(count * 4, true);
-        counter_count = count;
-    }
 }
 
 void marin_gpu::launched(int kind, double bytes) {
@@ -169,6 +164,9 @@ marin_status marin_gpu_new(marin_gpu **out) {
         if (arch.rfind("gfx950", 0) != 0)
             throw Error(MARIN_UNAVAILABLE, "device 0 is " + arch + "; this library is built for gfx950 only");
         HIP_CHECK(hipSetDevice(0));
+        // Registered after the runtime is up, so it runs before the runtime's exit handlers.
+        static std::once_flag once;
+        std::call_once(once, [] { std::atexit(destroy_graphs_at_exit); });
         auto *g = new marin_gpu();
         g->device = 0;
         g->cu_count = prop.multiProcessorCount;
@@ -187,12 +185,6 @@ void marin_gpu_free(marin_gpu *g) {
     if (!g || g->closing) return;
     (void)hipStreamSynchronize(g->stream);
     forget_rope_frequencies(g);
-    g->release(g->split);
-    g->split = nullptr;
-    g->release(g->partials);
-    g->partials = nullptr;
-    g->release(g->counters);
-    g->counters = nullptr;
     g->closing = true;
     if (g->live == 0) g->destroy();
 }

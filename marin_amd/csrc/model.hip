@@ -5,9 +5,12 @@
 //    silu(gate) * up straight into the f16 split the down projection reads;
 //  - the o and down projections add into the residual stream in their epilogue;
 //  - q/k RMSNorm, RoPE and the KV-cache store are one kernel;
-//  - every norm writes the f16 split its GEMV consumes, and attention's merge writes o_proj's split.
-// Positions live in device memory (pos, ctx), so a decode step has no host arguments and replays as a HIP graph:
-// the greedy loop picks the next token on the device and feeds it back without a host round trip.
+//  - the input RMSNorm, post-attention RMSNorm and final norm run inside the prologue of the product that consumes
+//    them (each block normalizes the row while its first weights are in flight), so no norm kernel remains;
+//  - the greedy choice is an atomic max in the output head's epilogue, and one small kernel then records the token,
+//    advances the positions and embeds the token for the next step.
+// A decode step is 7 launches per layer plus 2. Positions live in device memory (pos, ctx), so a step has no host
+// arguments and replays as a HIP graph: the greedy loop never returns to the host.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -17,52 +20,13 @@
 
 #include "attention.hpp"
 #include "ops.hpp"
-#include "quant.hpp"
+#include "gemv.hpp"
 
 using namespace marin;
 
 namespace marin {
 
-constexpr size_t CHUNK = MAX_GEMV_TOKENS;  // tokens per pass through the layers
-
-// RMSNorm of rows [row0, row0 + n) of x into the f16 split (per-token power-of-two scaling), one block per row.
-__global__ __launch_bounds__(256) void rms_norm_split_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                             int dim, float eps, _Float16 *__restrict__ data,
-                                                             float *__restrict__ inv) {
-    const int t = blockIdx.x;
-    const float *row = x + (size_t)t * dim;
-    __shared__ float red[4];
-    __shared__ float redm[4];
-    float s = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += 256) s += row[i] * row[i];
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
-    const float total = (red[0] + red[1]) + (red[2] + red[3]);
-    const float scale = 1.0f / sqrtf(total / (float)dim + eps);
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += 256) m = fmaxf(m, fabsf(row[i] * scale * w[i]));
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
-    float up = 1.0f, down = 1.0f;
-    if (m > 0.0f && m < INFINITY) {
-        int e;
-        (void)frexpf(m, &e);
-        int sh = 15 - e;
-        sh = sh > 100 ? 100 : (sh < -100 ? -100 : sh);
-        up = ldexpf(1.0f, sh);
-        down = ldexpf(1.0f, -sh);
-    }
-    for (int i = threadIdx.x; i < dim; i += 256) {
-        const float y = row[i] * scale * w[i] * up;
-        const _Float16 hi = (_Float16)y;
-        data[((size_t)t * 2) * dim + i] = hi;
-        data[((size_t)t * 2 + 1) * dim + i] = (_Float16)(y - (float)hi);
-    }
-    if (threadIdx.x == 0) inv[t] = down;
-}
+constexpr size_t CHUNK = GEMV_TOKENS;  // tokens per pass through the layers
 
 // Per (token, head): q heads get RMSNorm(q_norm) + RoPE into q; k heads RMSNorm(k_norm) + RoPE into the cache; v heads
 // go to the cache as they are. grid (tokens, heads + 2 * kv_heads), 64 threads; thread i takes the pairs (i, i + hd/2).
@@ -159,56 +123,38 @@ __global__ __launch_bounds__(64) void qk_norm_rope_store(const float *__restrict
     }
 }
 
-// Greedy choice (sampler/src/lib.rs:40-48): the largest logit under f32's total order, the lowest id on ties. One
-// block; the winner goes to ids[0] (the next pass's input) and to tokens_out[step] with step = state[2]. Then the
-// state advances: pos += count, ctx = pos + 1, step += 1.
-__device__ __forceinline__ int total_key(float v) {
-    const int b = __float_as_int(v);
-    return b ^ (int)(((unsigned)(b >> 31)) >> 1);
-}
-
-__global__ __launch_bounds__(1024) void argmax_advance(const float *__restrict__ logits, int n, uint32_t *ids,
-                                                       uint32_t *tokens_out, uint32_t *state, int count) {
-    int best_key = INT_MIN, best = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const int k = total_key(logits[i]);
-        if (k > best_key) {
-            best_key = k;
-            best = i;
-        }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const int ok = __shfl_xor(best_key, o), oi = __shfl_xor(best, o);
-        if (ok > best_key || (ok == best_key && oi < best)) {
-            best_key = ok;
-            best = oi;
-        }
-    }
-    __shared__ int keys[16], idx[16];
-    if ((threadIdx.x & 63) == 0) {
-        keys[threadIdx.x >> 6] = best_key;
-        idx[threadIdx.x >> 6] = best;
-    }
-    __syncthreads();
+// One decode step's bookkeeping, after the output head left the greedy choice in *best as (total-order key, ~id)
+// (sampler/src/lib.rs:40-48: largest logit, lowest id on ties): record the token, clear the choice for the next
+// head, advance the state (pos += 1, ctx = pos + 1, step += 1) and embed the token's table row into hidden.
+__global__ __launch_bounds__(512) void advance(unsigned long long *best, uint32_t *ids, uint32_t *tokens_out,
+                                               uint32_t *state, const uint8_t *__restrict__ codes,
+                                               const float *__restrict__ scales, float *__restrict__ hidden, int cols,
+                                               int group) {
+    __shared__ uint32_t id_s;
     if (threadIdx.x == 0) {
-        int k = keys[0], b = idx[0];
-        for (int w = 1; w < 16; ++w)
-            if (keys[w] > k || (keys[w] == k && idx[w] < b)) {
-                k = keys[w];
-                b = idx[w];
-            }
-        ids[0] = (uint32_t)b;
-        if (tokens_out) tokens_out[state[2]] = (uint32_t)b;
-        state[0] += (uint32_t)count;
+        const uint32_t id = 0xffffffffu - (uint32_t)(*best & 0xffffffffull);
+        *best = 0ull;
+        ids[0] = id;
+        tokens_out[state[2]] = id;
+        state[0] += 1;
         state[1] = state[0] + 1;
         state[2] += 1;
+        id_s = id;
     }
+    __syncthreads();
+    const size_t row = id_s;
+    const int groups = cols / group;
+    const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
+    for (int i = threadIdx.x; i < cols; i += blockDim.x)
+        hidden[i] = (float)(int8_t)codes[row * cols + i] * srow[(i / group) * 16];
 }
 
-// Sets the device state for a pass of `count` tokens at `pos`: pos, ctx = pos + count.
-__global__ void set_state(uint32_t *state, uint32_t pos, uint32_t count) {
+// Sets the device state for a pass of `count` tokens at `pos` (pos, ctx = pos + count) and clears the greedy choice
+// the pass's output head will make.
+__global__ void set_state(uint32_t *state, uint32_t pos, uint32_t count, unsigned long long *best) {
     state[0] = pos;
     state[1] = pos + count;
+    *best = 0ull;
 }
 
 __global__ void embed_device_ids(const uint8_t *__restrict__ codes, const float *__restrict__ scales,
@@ -243,9 +189,9 @@ struct marin_qwen3_cache {
     marin_qwen3 *model = nullptr;
     marin_kv *kv = nullptr;
     // device workspace, CHUNK tokens
-    float *hidden = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr;
-    void *split_h = nullptr, *split_ctx = nullptr, *split_act = nullptr;
+    float *hidden = nullptr, *qkv = nullptr, *q = nullptr, *ctx = nullptr, *act = nullptr, *logits = nullptr;
     uint32_t *ids = nullptr, *state = nullptr, *tokens_out = nullptr;
+    unsigned long long *best = nullptr;  // greedy choice of the last pass (key, ~id)
     size_t tokens_cap = 0;
     float *attn_partials = nullptr;
     size_t attn_partial_floats = 0;
@@ -336,30 +282,32 @@ static uint64_t synth_stream(int layer, int tensor) {
 
 static void free_cache_graph(marin_qwen3_cache *c) {
     if (c->graph) {
+        unregister_graph(c->graph);
         (void)hipGraphExecDestroy(c->graph);
         c->graph = nullptr;
     }
 }
 
-// One pass over `n` (<= CHUNK) tokens whose ids are already in c->ids, at the position in c->state. Writes the last
-// token's logits. `max_ctx` bounds the context for the attention grid.
+// One pass over `n` (<= CHUNK) tokens at the position in c->state, whose embeddings are already in c->hidden. Writes
+// the last token's logits and its greedy choice. `max_ctx` bounds the context for the attention grid; `host_ctx`
+// (when known) only feeds launch accounting.
 static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx, size_t host_ctx = 0) {
     marin_gpu *g = m->gpu;
     const auto &cfg = m->cfg;
     const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd(), F = cfg.ffn;
-    SplitView sh = split_view(c->split_h, n, H), sc = split_view(c->split_ctx, n, qd), sa = split_view(c->split_act, n, F);
-    embed_device_ids<<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(m->embed->codes, (const float *)m->embed->scales,
-                                                                      c->ids, c->hidden, (int)H, (int)cfg.group);
-    g->launched();
     for (size_t l = 0; l < m->layers.size(); ++l) {
         Layer &L = m->layers[l];
-        rms_norm_split_kernel<<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(c->hidden, L.input_norm, (int)H,
-                                                                              cfg.rms_eps, sh.data, sh.inv);
-        g->launched();
-        EpiArgs e;
-        e.y = c->qkv;
-        e.y_stride = qd + 2 * kvd;
-        launch_gemv_mfma(g, L.qkv, sh, n, EPI_F32, e);
+        GemvIn norm_in;
+        norm_in.mode = IN_NORM;
+        norm_in.x = c->hidden;
+        norm_in.x_stride = H;
+        norm_in.norm = L.input_norm;
+        norm_in.eps = cfg.rms_eps;
+        GemvOut qkv_out;
+        qkv_out.mode = OUT_F32;
+        qkv_out.y = c->qkv;
+        qkv_out.y_stride = qd + 2 * kvd;
+        launch_gemv(g, L.qkv, norm_in, qkv_out, n);
         const KvGeom geom = c->kv->geom(l);
         dim3 grid((unsigned)n, (unsigned)(cfg.heads + 2 * cfg.kv_heads));
 #define MARIN_QK(F)                                                                                                 \
@@ -374,9 +322,8 @@ static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx,
         AttentionArgs a{};
         a.q = c->q;
         a.q_bf16 = false;
-        a.out = sc.data;
-        a.out_kind = 2;
-        a.split_inv = sc.inv;
+        a.out = c->ctx;
+        a.out_kind = 0;
         a.tables = c->kv->page_ptrs;
         a.table_stride = 0;
         a.ctx = c->state + 1;
@@ -390,29 +337,40 @@ static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx,
         a.partial_floats = c->attn_partial_floats;
         a.bytes_hint = (double)host_ctx * 2 * kvd * kv_elem_bytes(c->kv->format) + 2.0 * n * qd * 4;
         launch_attention(g, a);
-        EpiArgs eo;
-        eo.y = c->hidden;
-        eo.y_stride = H;
-        launch_gemv_mfma(g, L.o, sc, n, EPI_ADD, eo);
-        rms_norm_split_kernel<<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(c->hidden, L.post_norm, (int)H,
-                                                                              cfg.rms_eps, sh.data, sh.inv);
-        g->launched();
-        EpiArgs eg;
-        eg.split_out = sa;
-        launch_gemv_mfma(g, L.gate_up, sh, n, EPI_SILU_SPLIT, eg);
-        EpiArgs ed;
-        ed.y = c->hidden;
-        ed.y_stride = H;
-        launch_gemv_mfma(g, L.down, sa, n, EPI_ADD, ed);
+        GemvIn ctx_in;
+        ctx_in.mode = IN_F32;
+        ctx_in.x = c->ctx;
+        ctx_in.x_stride = qd;
+        GemvOut add_out;
+        add_out.mode = OUT_ADD;
+        add_out.y = c->hidden;
+        add_out.y_stride = H;
+        launch_gemv(g, L.o, ctx_in, add_out, n);
+        GemvIn post_in = norm_in;
+        post_in.norm = L.post_norm;
+        GemvOut silu_out;
+        silu_out.mode = OUT_SILU;
+        silu_out.y = c->act;
+        silu_out.y_stride = F;
+        launch_gemv(g, L.gate_up, post_in, silu_out, n);
+        GemvIn act_in;
+        act_in.mode = IN_F32;
+        act_in.x = c->act;
+        act_in.x_stride = F;
+        launch_gemv(g, L.down, act_in, add_out, n);
     }
-    SplitView last = split_view(c->split_h, 1, H);
-    rms_norm_split_kernel<<<dim3(1), dim3(256), 0, g->stream>>>(c->hidden + (n - 1) * H, m->final_norm, (int)H,
-                                                                cfg.rms_eps, last.data, last.inv);
-    g->launched();
-    EpiArgs el;
-    el.y = c->logits;
-    el.y_stride = cfg.vocab;
-    launch_gemv_mfma(g, m->head(), last, 1, EPI_F32, el);
+    GemvIn last;
+    last.mode = IN_NORM;
+    last.x = c->hidden + (n - 1) * H;
+    last.x_stride = H;
+    last.norm = m->final_norm;
+    last.eps = cfg.rms_eps;
+    GemvOut head;
+    head.mode = OUT_F32;
+    head.y = c->logits;
+    head.y_stride = cfg.vocab;
+    head.argmax = c->best;
+    launch_gemv(g, m->head(), last, head, 1);
 }
 
 static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n) {
@@ -427,7 +385,10 @@ static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids
         const size_t nt = std::min(CHUNK, n - t0);
         void *staged = g->stage(ids + t0, nt * 4);
         HIP_CHECK(hipMemcpyAsync(c->ids, staged, nt * 4, hipMemcpyHostToDevice, g->stream));
-        set_state<<<1, 1, 0, g->stream>>>(c->state, (uint32_t)(start + t0), (uint32_t)nt);
+        set_state<<<1, 1, 0, g->stream>>>(c->state, (uint32_t)(start + t0), (uint32_t)nt, c->best);
+        g->launched();
+        embed_device_ids<<<dim3((unsigned)nt), dim3(256), 0, g->stream>>>(
+            m->embed->codes, (const float *)m->embed->scales, c->ids, c->hidden, (int)m->cfg.hidden, (int)m->cfg.group);
         g->launched();
         pass(m, c, nt, start + t0 + nt);
         c->kv->len = start + t0 + nt;
@@ -531,17 +492,15 @@ marin_status marin_qwen3_cache_new(marin_qwen3 *m, size_t capacity, marin_kv_for
             c->qkv = (float *)g->alloc(CHUNK * (qd + 2 * kvd) * 4, true);
             c->q = (float *)g->alloc(CHUNK * qd * 4, true);
             c->logits = (float *)g->alloc(cfg.vocab * 4, true);
-            c->split_h = g->alloc(split_bytes(CHUNK, H), true);
-            c->split_ctx = g->alloc(split_bytes(CHUNK, qd), true);
-            c->split_act = g->alloc(split_bytes(CHUNK, cfg.ffn), true);
+            c->ctx = (float *)g->alloc(CHUNK * qd * 4, true);
+            c->act = (float *)g->alloc(CHUNK * cfg.ffn * 4, true);
+            c->best = (unsigned long long *)g->alloc(8, true);
             c->ids = (uint32_t *)g->alloc(CHUNK * 4, true);
             c->state = (uint32_t *)g->alloc(16, true);
+            c->tokens_out = (uint32_t *)g->alloc(std::max<size_t>(capacity, 1) * 4, true);
+            c->tokens_cap = std::max<size_t>(capacity, 1);
             c->attn_partial_floats = attention_partial_floats(1, CHUNK, cfg.heads, cfg.head_dim, capacity, g->cu_count);
             c->attn_partials = (float *)g->alloc(c->attn_partial_floats * 4, false);
-            // The GEMV cross-block scratch for every shape this model uses, sized now so no pass allocates.
-            size_t most_rows = std::max({m->layers[0].qkv->rows_padded, m->layers[0].gate_up->rows_padded,
-                                         m->head()->rows_padded});
-            g->ensure_partials(64 * CHUNK * most_rows, most_rows / 16 + 1);
         } catch (...) {
             marin_qwen3_cache_free(c.release());
             throw;
@@ -556,8 +515,9 @@ void marin_qwen3_cache_free(marin_qwen3_cache *c) {
     (void)hipStreamSynchronize(g->stream);
     free_cache_graph(c);
     marin_kv_free(c->kv);
-    for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->q, (void *)c->logits, c->split_h, c->split_ctx,
-                    c->split_act, (void *)c->ids, (void *)c->state, (void *)c->attn_partials, (void *)c->tokens_out})
+    for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->q, (void *)c->logits, (void *)c->ctx, (void *)c->act,
+                    (void *)c->best, (void *)c->ids, (void *)c->state, (void *)c->attn_partials,
+                    (void *)c->tokens_out})
         g->release(p);
     delete c;
 }
@@ -576,7 +536,9 @@ marin_status marin_qwen3_forward(marin_qwen3 *m, marin_qwen3_cache *c, const uin
 // One decode step on the device: choose the next token from the last pass's logits, then run it through the model.
 static void decode_step(marin_qwen3 *m, marin_qwen3_cache *c, size_t host_ctx) {
     marin_gpu *g = m->gpu;
-    argmax_advance<<<1, 1024, 0, g->stream>>>(c->logits, (int)m->cfg.vocab, c->ids, c->tokens_out, c->state, 1);
+    advance<<<1, 512, 0, g->stream>>>(c->best, c->ids, c->tokens_out, c->state, m->embed->codes,
+                                      (const float *)m->embed->scales, c->hidden, (int)m->cfg.hidden,
+                                      (int)m->cfg.group);
     g->launched();
     pass(m, c, 1, c->kv->capacity, host_ctx);
 }
@@ -623,6 +585,7 @@ static void decode(marin_qwen3 *m, marin_qwen3_cache *c, size_t steps, uint32_t 
             hipError_t e = hipGraphInstantiate(&c->graph, graph, nullptr, nullptr, 0);
             (void)hipGraphDestroy(graph);
             hip_check(e, "hipGraphInstantiate");
+            register_graph(c->graph);
         }
         for (size_t s = 0; s < steps; ++s) {
             HIP_CHECK(hipGraphLaunch(c->graph, g->stream));

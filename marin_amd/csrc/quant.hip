@@ -1,381 +1,16 @@
-// Quantized linear layers on CDNA4 (crates/cuda/src/quant.rs + quant.cu of the reference, redesigned for gfx950).
-//
-// The hot product streams int8 codes with one 16-byte load per lane, turns them into f16 exactly in registers
-// (0x6400 | (code ^ 0x80) is the f16 1024 + code + 128), and multiplies them on the matrix cores
-// (v_mfma_f32_16x16x32_f16) against the activations split into f16 parts: x * 2^s = hi + lo (+ mid), each part one
-// B column. f16 holds every code exactly and the parts carry 22 (33) bits of each activation, so the products are
-// f32-grade while the conversion costs about one VALU op per weight instead of a convert and an FMA. Partial sums are
-// f32 in the MFMA accumulators; each 64-column window is scaled by its group's scale once.
+// Quantized matrices on the device (crates/cuda/src/quant.rs + quant.cu of the reference, redesigned for gfx950):
+// upload and device layout, the general VALU product for layouts the matrix-core product does not take, the int8
+// embedding lookup, the on-device synthetic weights + quantizer, and the C ABI entry points. The matrix-core
+// product itself is in gemv.hip.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
 
-#include "quant.hpp"
+#include "gemv.hpp"
 
 namespace marin {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-size_t split_bytes(size_t tokens, size_t cols) {
-    size_t data = tokens * 3 * cols * sizeof(_Float16);  // room for three parts
-    data = (data + 255) & ~size_t(255);
-    return data + tokens * sizeof(float) + 256;
-}
-
-SplitView split_view(void *base, size_t tokens, size_t cols) {
-    SplitView v;
-    v.data = (_Float16 *)base;
-    size_t data = tokens * 3 * cols * sizeof(_Float16);
-    data = (data + 255) & ~size_t(255);
-    v.inv = (float *)((char *)base + data);
-    v.cols = cols;
-    v.tokens = tokens;
-    return v;
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Activation split: one block per token. With scale_tokens the token is first scaled by the power of two that puts
-// its largest magnitude in [2^14, 2^15), which keeps every part inside f16's normal range; inv undoes it exactly.
-// Part p of token t lives at data[(t * parts + p) * cols].
-template <int PARTS, typename In>
-__global__ __launch_bounds__(256) void split_kernel(const In *__restrict__ x, size_t cols, _Float16 *__restrict__ data,
-                                                     float *__restrict__ inv, int scale_tokens) {
-    const size_t t = blockIdx.x;
-    const In *row = x + t * cols;
-    __shared__ float red[4];
-    float scale = 1.0f, undo = 1.0f;
-    if (scale_tokens) {
-        float m = 0.0f;
-        for (size_t i = threadIdx.x; i < cols; i += 256) {
-            float v;
-            if constexpr (sizeof(In) == 4) v = row[i];
-            else v = __uint_as_float((unsigned)row[i] << 16);
-            m = fmaxf(m, fabsf(v));
-        }
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-        __syncthreads();
-        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        if (m > 0.0f && m < INFINITY) {
-            int e;
-            (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1)
-            int s = 15 - e;
-            s = s > 100 ? 100 : (s < -100 ? -100 : s);
-            scale = ldexpf(1.0f, s);
-            undo = ldexpf(1.0f, -s);
-        }
-    }
-    for (size_t i = threadIdx.x; i < cols; i += 256) {
-        float v;
-        if constexpr (sizeof(In) == 4) v = row[i];
-        else v = __uint_as_float((unsigned)row[i] << 16);
-        v *= scale;
-        _Float16 hi = (_Float16)v;
-        float rest = v - (float)hi;
-        _Float16 mid = (_Float16)rest;
-        data[(t * PARTS + 0) * cols + i] = hi;
-        data[(t * PARTS + 1) * cols + i] = mid;
-        if constexpr (PARTS == 3) data[(t * PARTS + 2) * cols + i] = (_Float16)(rest - (float)mid);
-    }
-    if (threadIdx.x == 0) inv[t] = undo;
-}
-
-void launch_split_f32(marin_gpu *g, const float *x, size_t tokens, size_t cols, SplitView out, bool scale_tokens) {
-    if (!tokens) return;
-    split_kernel<2, float><<<dim3((unsigned)tokens), dim3(256), 0, g->stream>>>(x, cols, out.data, out.inv,
-                                                                                scale_tokens ? 1 : 0);
-    g->launched();
-}
-
-static void launch_split3_f32(marin_gpu *g, const float *x, size_t tokens, size_t cols, SplitView out) {
-    if (!tokens) return;
-    split_kernel<3, float><<<dim3((unsigned)tokens), dim3(256), 0, g->stream>>>(x, cols, out.data, out.inv, 1);
-    g->launched();
-}
-
-void launch_split_bf16(marin_gpu *g, const uint16_t *x, size_t tokens, size_t cols, SplitView out) {
-    if (!tokens) return;
-    split_kernel<2, uint16_t><<<dim3((unsigned)tokens), dim3(256), 0, g->stream>>>(x, cols, out.data, out.inv, 1);
-    g->launched();
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// int8 codes -> f16, exactly: byte b becomes the f16 with bits 0x6400 | (b ^ 0x80), i.e. 1024 + code + 128, and one
-// packed subtraction of 1152 leaves the code.
-__device__ __forceinline__ half2v pair_f16(uint32_t word, int shift) {
-    const uint32_t lo = (word >> shift) & 0xffu, hi = (word >> (shift + 8)) & 0xffu;
-    const uint32_t bits = lo | (hi << 16) | 0x64006400u;
-    return __builtin_bit_cast(half2v, bits) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
-}
-
-__device__ __forceinline__ half8 decode8(uint32_t w0, uint32_t w1) {
-    w0 ^= 0x80808080u;
-    w1 ^= 0x80808080u;
-    const half2v a = pair_f16(w0, 0), b = pair_f16(w0, 16), c = pair_f16(w1, 0), d = pair_f16(w1, 16);
-    return (half8){a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
-}
-
-template <typename ST>
-__device__ __forceinline__ floatx4 load_scale4(const ST *p) {
-    if constexpr (sizeof(ST) == 4) {
-        return *reinterpret_cast<const floatx4 *>(p);
-    } else {
-        const uint2 u = *reinterpret_cast<const uint2 *>(p);
-        return (floatx4){__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
-                         __uint_as_float(u.y & 0xffff0000u)};
-    }
-}
-
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
-
-constexpr int WAVES = 4;
-constexpr int MAX_COLS = 16;  // B columns of one MFMA
-
-// One block: 16*RT rows (RT tiles of 16) of the matrix, the windows [w0, w1) of 64 columns split into contiguous
-// runs across its four waves. Lane l of a wave loads 16 code bytes of row (l % 16) at column 64w + 16(l / 16) and the
-// matching 8+8 f16 of every B column c = l % 16 < used; the MFMA's D gives lane l rows 4(l/16)..+3 of column l % 16.
-// Grid: x = row blocks, y = column splits (kb). With more than one split, each block leaves its sums in `partials`
-// and the last block to arrive at a row block's counter adds them in split order, so results do not depend on
-// timing; that block also puts the counter back to zero.
-template <int RT, typename ST, int EPI, int PARTS, bool ONE>
-__global__ __launch_bounds__(256) void gemv_i8_mfma(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
-                                                   const _Float16 *__restrict__ xs, const float *__restrict__ xinv,
-                                                   int tokens_arg, int rows, int rows_padded, int cols, int group,
-                                                   int windows_per_split, float *__restrict__ partials,
-                                                   unsigned *__restrict__ counters, EpiArgs epi) {
-    // ONE: a single token (decode), known at compile time; otherwise up to MAX_GEMV_TOKENS.
-    const int tokens = ONE ? 1 : tokens_arg;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = lane & 15, q = lane >> 4;
-    const int used = tokens * PARTS;
-    const int total_windows = cols >> 6;
-    const int splits = gridDim.y;
-    const int kw0 = blockIdx.y * windows_per_split;
-    const int kw1 = min(total_windows, kw0 + windows_per_split);
-    const int span = kw1 > kw0 ? kw1 - kw0 : 0;
-    const int per_wave = (span + WAVES - 1) / WAVES;
-    const int w0 = kw0 + min(span, wave * per_wave);
-    const int w1 = kw0 + min(span, (wave + 1) * per_wave);
-    const int groups = cols / group;
-    const int tile0 = blockIdx.x * RT;
-
-    floatx4 total[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) total[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
-
-    const uint8_t *arow[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) arow[r] = codes + (size_t)((tile0 + r) * 16 + c) * cols + 16 * q;
-    const _Float16 *brow = xs + (size_t)c * cols + 16 * q;
-    const bool bcol = c < used;
-    const ST *srow[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) srow[r] = scales + (size_t)(tile0 + r) * groups * 16 + 4 * q;
-
-    constexpr int D = 4;  // windows in flight per wave
-    int w = w0;
-    for (; w + D <= w1; w += D) {
-        u32x4 a[D][RT];
-        half8 b[D][2];
-        floatx4 s[D][RT];
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int col = (w + d) * 64;
-#pragma unroll
-            for (int r = 0; r < RT; ++r) a[d][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(arow[r] + col));
-            if (bcol) {
-                b[d][0] = *reinterpret_cast<const half8 *>(brow + col);
-                b[d][1] = *reinterpret_cast<const half8 *>(brow + col + 8);
-            } else {
-                b[d][0] = (half8){0, 0, 0, 0, 0, 0, 0, 0};
-                b[d][1] = b[d][0];
-            }
-            const int gi = col / group;
-#pragma unroll
-            for (int r = 0; r < RT; ++r) s[d][r] = load_scale4(srow[r] + gi * 16);
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                floatx4 acc = (floatx4){0.f, 0.f, 0.f, 0.f};
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8(a[d][r].x, a[d][r].y), b[d][0], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8(a[d][r].z, a[d][r].w), b[d][1], acc, 0, 0, 0);
-                total[r] += acc * s[d][r];
-            }
-    }
-    for (; w < w1; ++w) {
-        const int col = w * 64;
-        half8 b0 = (half8){0, 0, 0, 0, 0, 0, 0, 0}, b1 = b0;
-        if (bcol) {
-            b0 = *reinterpret_cast<const half8 *>(brow + col);
-            b1 = *reinterpret_cast<const half8 *>(brow + col + 8);
-        }
-        const int gi = col / group;
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(arow[r] + col));
-            const floatx4 s = load_scale4(srow[r] + gi * 16);
-            floatx4 acc = (floatx4){0.f, 0.f, 0.f, 0.f};
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8(a.x, a.y), b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8(a.z, a.w), b1, acc, 0, 0, 0);
-            total[r] += acc * s;
-        }
-    }
-
-    // Sum the waves (and the parts of each token) through LDS: red[wave][tile][column][row].
-    __shared__ float red[WAVES][RT][MAX_COLS][16];
-    __shared__ float vals[RT][MAX_GEMV_TOKENS][16];
-    __shared__ bool last;
-    if (c < used) {
-#pragma unroll
-        for (int r = 0; r < RT; ++r)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave][r][c][4 * q + i] = total[r][i];
-    }
-    __syncthreads();
-    const int outputs = RT * tokens * 16;
-    for (int o = threadIdx.x; o < outputs; o += 256) {
-        const int r = o / (tokens * 16), t = (o / 16) % tokens, row = o % 16;
-        float v = 0.0f;
-#pragma unroll
-        for (int wv = 0; wv < WAVES; ++wv) {
-            float part = 0.0f;
-#pragma unroll
-            for (int p = 0; p < PARTS; ++p) part += red[wv][r][t * PARTS + p][row];
-            v += part;
-        }
-        vals[r][t][row] = v * xinv[t];
-    }
-    __syncthreads();
-    if (splits > 1) {
-        const size_t stride = (size_t)rows_padded;
-        for (int o = threadIdx.x; o < outputs; o += 256) {
-            const int r = o / (tokens * 16), t = (o / 16) % tokens, row = o % 16;
-            partials[((size_t)blockIdx.y * tokens + t) * stride + (tile0 + r) * 16 + row] = vals[r][t][row];
-        }
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const unsigned prev = atomicAdd(&counters[blockIdx.x], 1u);
-            last = prev == (unsigned)(splits - 1);
-            if (last) counters[blockIdx.x] = 0u;
-        }
-        __syncthreads();
-        if (!last) return;
-        __threadfence();
-        for (int o = threadIdx.x; o < outputs; o += 256) {
-            const int r = o / (tokens * 16), t = (o / 16) % tokens, row = o % 16;
-            float v = 0.0f;
-            for (int k = 0; k < splits; ++k)
-                v += __builtin_nontemporal_load(&partials[((size_t)k * tokens + t) * stride + (tile0 + r) * 16 + row]);
-            vals[r][t][row] = v;
-        }
-        __syncthreads();
-    }
-    // Epilogue.
-    if constexpr (EPI == EPI_SILU_SPLIT) {
-        const int pairs = RT * 8 * tokens;
-        for (int o = threadIdx.x; o < pairs; o += 256) {
-            const int r = o / (tokens * 8), t = (o / 8) % tokens, pr = o % 8;
-            const int row = (tile0 + r) * 16 + 2 * pr;
-            if (row >= rows) continue;
-            const float a = silu_f(vals[r][t][2 * pr]) * vals[r][t][2 * pr + 1];
-            const size_t k = row >> 1, kc = epi.split_out.cols;
-            const _Float16 hi = (_Float16)a;
-            epi.split_out.data[(t * 2 + 0) * kc + k] = hi;
-            epi.split_out.data[(t * 2 + 1) * kc + k] = (_Float16)(a - (float)hi);
-            if (epi.act_out) epi.act_out[t * kc + k] = a;
-        }
-        if (blockIdx.x == 0 && threadIdx.x < (unsigned)tokens) epi.split_out.inv[threadIdx.x] = 1.0f;
-    } else {
-        for (int o = threadIdx.x; o < outputs; o += 256) {
-            const int r = o / (tokens * 16), t = (o / 16) % tokens, row16 = o % 16;
-            const int row = (tile0 + r) * 16 + row16;
-            if (row >= rows) continue;
-            const float v = vals[r][t][row16];
-            const size_t at = (size_t)t * epi.y_stride + row;
-            if constexpr (EPI == EPI_F32) reinterpret_cast<float *>(epi.y)[at] = v;
-            if constexpr (EPI == EPI_ADD) reinterpret_cast<float *>(epi.y)[at] += v;
-            if constexpr (EPI == EPI_BF16) {
-                const unsigned u = __float_as_uint(v);
-                const unsigned rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-                reinterpret_cast<uint16_t *>(epi.y)[at] = (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : rounded);
-            }
-        }
-    }
-}
-
-bool mfma_supported(const marin_quant_matrix *w) {
-    return w->bits == 8 && w->group % 64 == 0 && w->cols % 64 == 0;
-}
-
-// Chooses rows per block and column splits so a launch has about 2048+ waves with at least two windows each.
-template <typename ST, int EPI, int PARTS>
-static void launch_mfma_t(marin_gpu *g, const marin_quant_matrix *w, SplitView x, size_t tokens,
-                          const EpiArgs &args) {
-    const int windows = (int)(w->cols / 64);
-    const size_t tiles = w->rows_padded / 16;
-    int rt = tiles >= 4096 ? 4 : (tiles >= 1024 ? 2 : 1);
-    const size_t blocks_x = tiles / rt;
-    const size_t cu = (size_t)(g->cu_count > 0 ? g->cu_count : 256);
-    int splits = 1;
-    while (blocks_x * splits < 8 * cu && windows / (splits * 2) >= 2 * WAVES) splits *= 2;
-    const int per_split = (windows + splits - 1) / splits;
-    splits = (windows + per_split - 1) / per_split;
-    if (splits > 1) g->ensure_partials((size_t)splits * tokens * w->rows_padded, blocks_x);
-    const ST *sc = (const ST *)w->scales;
-    dim3 grid((unsigned)blocks_x, (unsigned)splits);
-#define MARIN_LAUNCH1(RT, ONE)                                                                                   \
-    gemv_i8_mfma<RT, ST, EPI, PARTS, ONE><<<grid, dim3(256), 0, g->stream>>>(                                   \
-        w->codes, sc, x.data, x.inv, (int)tokens, (int)w->rows, (int)w->rows_padded, (int)w->cols, (int)w->group, \
-        per_split, g->partials, g->counters, args)
-#define MARIN_LAUNCH(RT)                    \
-    do {                                    \
-        if (tokens == 1) MARIN_LAUNCH1(RT, true); \
-        else MARIN_LAUNCH1(RT, false);      \
-    } while (0)
-    if (rt == 4) MARIN_LAUNCH(4);
-    else if (rt == 2) MARIN_LAUNCH(2);
-    else MARIN_LAUNCH(1);
-#undef MARIN_LAUNCH
-#undef MARIN_LAUNCH1
-    // algorithmic bytes: codes + scales once, activations (f32) and outputs once
-    const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * w->groups() * (w->bf16_scales ? 2 : 4) +
-                         (double)tokens * w->cols * 4 + (double)tokens * w->rows * 4;
-    g->launched(marin_gpu::GEMV, bytes);
-}
-
-template <int EPI, int PARTS>
-static void launch_mfma_e(marin_gpu *g, const marin_quant_matrix *w, SplitView x, size_t tokens,
-                          const EpiArgs &args) {
-    if (w->bf16_scales) launch_mfma_t<uint16_t, EPI, PARTS>(g, w, x, tokens, args);
-    else launch_mfma_t<float, EPI, PARTS>(g, w, x, tokens, args);
-}
-
-void launch_gemv_mfma(marin_gpu *g, const marin_quant_matrix *w, SplitView x, size_t tokens, Epilogue epi,
-                      const EpiArgs &args) {
-    if (tokens == 0) return;
-    if (tokens > MAX_GEMV_TOKENS) throw Error(MARIN_UNSUPPORTED, "gemv tokens", MAX_GEMV_TOKENS, tokens);
-    switch (epi) {
-        case EPI_F32: launch_mfma_e<EPI_F32, 2>(g, w, x, tokens, args); break;
-        case EPI_ADD: launch_mfma_e<EPI_ADD, 2>(g, w, x, tokens, args); break;
-        case EPI_BF16: launch_mfma_e<EPI_BF16, 2>(g, w, x, tokens, args); break;
-        case EPI_SILU_SPLIT: launch_mfma_e<EPI_SILU_SPLIT, 2>(g, w, x, tokens, args); break;
-    }
-}
-
-static void launch_gemv_mfma_precise(marin_gpu *g, const marin_quant_matrix *w, SplitView x, size_t tokens,
-                                     float *y) {
-    EpiArgs a;
-    a.y = y;
-    a.y_stride = w->rows;
-    launch_mfma_e<EPI_F32, 3>(g, w, x, tokens, a);
-}
 
 // ---------------------------------------------------------------------------------------------------------------
 // General product for any group (a multiple of 32) and int4: one wave per row, a lane takes 8 consecutive columns per
@@ -407,9 +42,13 @@ __global__ __launch_bounds__(256) void gemv_valu(const uint8_t *__restrict__ cod
                 wv[i + 4] = (float)(int8_t)(u.y >> (8 * i));
             }
         } else {
+            // device int4 layout: byte e of each 4-byte word holds column e (low nibble) and column 4 + e (high)
             const uint32_t u = *reinterpret_cast<const uint32_t *>(crow + c / 2);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) wv[i] = (float)((int)((u >> (4 * i)) & 15u) - 8);
+            for (int i = 0; i < 4; ++i) {
+                wv[i] = (float)((int)((u >> (8 * i)) & 15u) - 8);
+                wv[i + 4] = (float)((int)((u >> (8 * i + 4)) & 15u) - 8);
+            }
         }
         float s;
         if constexpr (sizeof(ST) == 4) s = srow[(c / group) * 16];
@@ -597,10 +236,31 @@ void free_quant_matrix(marin_quant_matrix *m) {
     delete m;
 }
 
-void upload_rows(marin_quant_matrix *m, const uint8_t *codes, const void *scales, size_t src_rows, size_t dst_row0,
+// tensor::Quantized keeps int4 as byte j = column 2j (low nibble) | column 2j + 1 (high). The device keeps each
+// 8-column group as 4 bytes whose low nibbles are columns 0-3 and high nibbles columns 4-7, so two masks turn a
+// word into four bytes of consecutive columns.
+static void repack_int4(const uint8_t *src, uint8_t *dst, size_t bytes) {
+    for (size_t w = 0; w + 4 <= bytes; w += 4) {
+        uint8_t nib[8];
+        for (int j = 0; j < 4; ++j) {
+            nib[2 * j] = src[w + j] & 15u;
+            nib[2 * j + 1] = src[w + j] >> 4;
+        }
+        for (int e = 0; e < 4; ++e) dst[w + e] = (uint8_t)(nib[e] | (nib[4 + e] << 4));
+    }
+}
+
+void upload_rows(marin_quant_matrix *m, const uint8_t *codes_in, const void *scales, size_t src_rows, size_t dst_row0,
                  size_t dst_row_step) {
     marin_gpu *g = m->gpu;
     const size_t rb = m->row_bytes(), groups = m->groups(), es = m->bf16_scales ? 2 : 4;
+    std::vector<uint8_t> repacked;
+    const uint8_t *codes = codes_in;
+    if (m->bits == 4) {
+        repacked.resize(src_rows * rb);
+        repack_int4(codes_in, repacked.data(), repacked.size());
+        codes = repacked.data();
+    }
     // Codes: contiguous when the rows land contiguously, else row by row on the host side.
     std::vector<uint8_t> code_rows;
     if (dst_row_step == 1) {
@@ -630,26 +290,23 @@ void upload_rows(marin_quant_matrix *m, const uint8_t *codes, const void *scales
 }
 
 void matmul_f32(marin_gpu *g, const marin_quant_matrix *w, const float *x, size_t tokens, float *y, bool precise) {
+    (void)precise;  // the matrix-core product keeps 30 bits of every activation: f32-grade at every token count
     if (!tokens) return;
-    if (!mfma_supported(w)) {
+    if (!gemv_supported(w)) {
         launch_gemv_valu(g, w, x, tokens, y);
         return;
     }
-    const size_t chunk = precise ? 5 : MAX_GEMV_TOKENS;
-    g->ensure_split(split_bytes(chunk, w->cols));
-    for (size_t t0 = 0; t0 < tokens; t0 += chunk) {
-        const size_t nt = std::min(chunk, tokens - t0);
-        SplitView v = split_view(g->split, nt, w->cols);
-        if (precise) {
-            launch_split3_f32(g, x + t0 * w->cols, nt, w->cols, v);
-            launch_gemv_mfma_precise(g, w, v, nt, y + t0 * w->rows);
-        } else {
-            launch_split_f32(g, x + t0 * w->cols, nt, w->cols, v, true);
-            EpiArgs a;
-            a.y = y + t0 * w->rows;
-            a.y_stride = w->rows;
-            launch_gemv_mfma(g, w, v, nt, EPI_F32, a);
-        }
+    for (size_t t0 = 0; t0 < tokens; t0 += GEMV_TOKENS) {
+        const size_t nt = std::min<size_t>(GEMV_TOKENS, tokens - t0);
+        GemvIn in;
+        in.mode = IN_F32;
+        in.x = x + t0 * w->cols;
+        in.x_stride = w->cols;
+        GemvOut out;
+        out.mode = OUT_F32;
+        out.y = y + t0 * w->rows;
+        out.y_stride = w->rows;
+        launch_gemv(g, w, in, out, nt);
     }
 }
 
@@ -779,17 +436,18 @@ marin_status marin_matmul_quant_bf16(marin_gpu *g, const marin_quant_matrix *w, 
     return guard([&] {
         check_matmul(w, x, tokens, out, MARIN_BF16);
         if (!tokens || !w->rows || !w->cols) return;
-        if (!mfma_supported(w)) unsupported("bf16 product group/width (int8, group and cols multiples of 64)", 8,
-                                            (size_t)w->bits);
-        g->ensure_split(split_bytes(MAX_GEMV_TOKENS, w->cols));
-        for (size_t t0 = 0; t0 < tokens; t0 += MAX_GEMV_TOKENS) {
-            const size_t nt = std::min<size_t>(MAX_GEMV_TOKENS, tokens - t0);
-            SplitView v = split_view(g->split, nt, w->cols);
-            launch_split_bf16(g, (const uint16_t *)x->data + t0 * w->cols, nt, w->cols, v);
-            EpiArgs a;
-            a.y = (uint16_t *)out->data + t0 * w->rows;
-            a.y_stride = w->rows;
-            launch_gemv_mfma(g, w, v, nt, EPI_BF16, a);
+        if (!gemv_supported(w)) unsupported("bf16 product layout (group and cols multiples of 64)", 64, w->group);
+        for (size_t t0 = 0; t0 < tokens; t0 += GEMV_TOKENS) {
+            const size_t nt = std::min<size_t>(GEMV_TOKENS, tokens - t0);
+            GemvIn in;
+            in.mode = IN_BF16;
+            in.x = (const uint16_t *)x->data + t0 * w->cols;
+            in.x_stride = w->cols;
+            GemvOut o;
+            o.mode = OUT_BF16;
+            o.y = (uint16_t *)out->data + t0 * w->rows;
+            o.y_stride = w->rows;
+            launch_gemv(g, w, in, o, nt);
         }
     });
 }

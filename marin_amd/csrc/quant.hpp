@@ -23,38 +23,7 @@ struct marin_quant_matrix {
 namespace marin {
 
 constexpr size_t ROW_PAD = 64;
-constexpr int MAX_GEMV_TOKENS = 8;
 
-// f16 hi/lo split of activations: data [tokens][2][cols] then f32 inv[tokens] (the per-token power of two that undoes
-// the scaling applied before the split). The MFMA product reads its B operand from here.
-struct SplitView {
-    _Float16 *data;
-    float *inv;
-    size_t cols, tokens;
-};
-size_t split_bytes(size_t tokens, size_t cols);
-SplitView split_view(void *base, size_t tokens, size_t cols);
-
-enum Epilogue : int {
-    EPI_F32 = 0,        // y[t][r] = v
-    EPI_ADD = 1,        // y[t][r] += v (residual)
-    EPI_BF16 = 2,       // y bf16
-    EPI_SILU_SPLIT = 3  // rows (2i, 2i+1) = (gate_i, up_i): silu(gate)*up -> f16 split of [tokens][rows/2]
-};
-
-struct EpiArgs {
-    void *y = nullptr;       // EPI_F32/ADD/BF16: [tokens][y_stride]
-    size_t y_stride = 0;     // elements between tokens of y
-    SplitView split_out{};   // EPI_SILU_SPLIT
-    float *act_out = nullptr; // EPI_SILU_SPLIT: optional f32 copy [tokens][rows/2]
-};
-
-// Launchers (all on gpu->stream, no synchronization).
-void launch_split_f32(marin_gpu *g, const float *x, size_t tokens, size_t cols, SplitView out, bool scale_tokens);
-void launch_split_bf16(marin_gpu *g, const uint16_t *x, size_t tokens, size_t cols, SplitView out);
-bool mfma_supported(const marin_quant_matrix *w);
-void launch_gemv_mfma(marin_gpu *g, const marin_quant_matrix *w, SplitView x, size_t tokens, Epilogue epi,
-                      const EpiArgs &args);
 void launch_gemv_valu(marin_gpu *g, const marin_quant_matrix *w, const float *x, size_t tokens, float *y);
 void launch_embed_q8(marin_gpu *g, const marin_quant_matrix *w, const uint32_t *ids, size_t n, float *out);
 // Fills a matrix from the synthetic generator (seed, stream) and quantizes it int8 with the reference's rule.
@@ -68,8 +37,8 @@ void free_quant_matrix(marin_quant_matrix *m);
 void upload_rows(marin_quant_matrix *m, const uint8_t *codes, const void *scales, size_t src_rows, size_t dst_row0,
                  size_t dst_row_step);
 
-// The product every entry point takes: splits x into the workspace and runs the MFMA kernel when the matrix
-// allows, the VALU kernel otherwise. tokens may exceed MAX_GEMV_TOKENS (chunks of it).
+// The product every f32 entry point takes: the matrix-core kernel when the matrix allows, the VALU kernel otherwise.
+// Any token count (chunks of GEMV_TOKENS).
 void matmul_f32(marin_gpu *g, const marin_quant_matrix *w, const float *x, size_t tokens, float *y, bool precise);
 
 }  // namespace marin
