@@ -96,11 +96,15 @@ __device__ __forceinline__ int total_key(float v) {
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
-// BITS: 8 or 4. RT: 16-row tiles per block. UW: 64-column windows per unit (2 when a group spans 128 columns).
+// BITS: 8 or 4. RT: 16-row tiles per tile block. UW: 64-column windows per unit (2 when a group spans 128 columns).
+// The grid is persistent: block b takes tile blocks b, b + gridDim.x, ... and pays for its prologue once. A wave's
+// work is one sequence of (segment, unit) steps, a segment being one tile block (times one column chunk when the
+// limbs are staged in chunks); its ring of code loads runs across segment ends, so the next tile's codes are in
+// flight while a tile's sums are reduced and written.
 template <int BITS, int RT, int UW, typename ST, bool ONE>
 __global__ __launch_bounds__(64 * GW) void gemv_q(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                   GemvIn in, GemvOut out, int tokens_arg, int rows, int cols,
-                                                  int group, int kc) {
+                                                  int group, int kc, int tile_blocks) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int tokens = ONE ? 1 : tokens_arg;
     const int lane = threadIdx.x & 63;
@@ -108,50 +112,63 @@ __global__ __launch_bounds__(64 * GW) void gemv_q(const uint8_t *__restrict__ co
     const int c = lane & 15, q = lane >> 4;
     const int used = tokens * LIMBS;
     const int groups = cols / group;
-    const int tile0 = blockIdx.x * RT;
     constexpr int UC = 64 * UW;  // columns per unit
     const int units = cols / UC;
     constexpr int CB = BITS == 8 ? 16 : 8;  // code bytes per lane per window
+    constexpr int PFU = pfu(RT);
     const size_t row_bytes = BITS == 8 ? (size_t)cols : (size_t)cols / 2;
 
-    // LDS: token stats | scales [RT][groups][16] | limbs [tokens*4][kc] | column sums [kc/UC][16] (int4)
+    // LDS: token stats | limbs [tokens*4][kc] | column sums [kc/UC][16] (int4) | red [GW][RT][16][16] | vals
     TokenStat *stat = reinterpret_cast<TokenStat *>(lds);
     float *red8 = reinterpret_cast<float *>(lds + 4 * sizeof(TokenStat));
-    ST *sc_l = reinterpret_cast<ST *>(lds + 256);
-    const size_t sc_bytes = ((size_t)RT * groups * 16 * sizeof(ST) + 15) & ~size_t(15);
-    int8_t *limbs = reinterpret_cast<int8_t *>(lds + 256 + sc_bytes);
-    int *colsum = reinterpret_cast<int *>(lds + 256 + sc_bytes + (size_t)used * kc);
+    int8_t *limbs = reinterpret_cast<int8_t *>(lds + 256);
+    int *colsum = reinterpret_cast<int *>(lds + 256 + (size_t)used * kc);
+    const size_t cs_bytes = BITS == 4 ? (size_t)(kc / UC) * 16 * 4 : 0;
+    float *red = reinterpret_cast<float *>(lds + 256 + (size_t)used * kc + cs_bytes);
+    float *vals = red + GW * RT * 16 * 16;
 
-    // ---- codes in flight first
-    const uint8_t *arow[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) arow[r] = codes + (size_t)((tile0 + r) * 16 + c) * row_bytes + (CB * q);
-    constexpr int PFU = pfu(RT);
-    const int n = units > wave ? (units - wave + GW - 1) / GW : 0;
-    const int last = n > 0 ? n - 1 : 0;
+    // ---- the wave's step sequence
+    const int chunks = (cols + kc - 1) / kc;
+    const int upc = kc / UC;                   // units per chunk
+    const int n_uni = (upc + GW - 1) / GW;     // steps per segment (the same for every wave)
+    const int my_tbs = tile_blocks > (int)blockIdx.x ? (tile_blocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+    const int total_s = my_tbs * chunks * n_uni;
+    // step s -> tile block, chunk, chunk-local unit (clamped to a real unit for loads)
+    auto step_unit = [&](int st, int &tile0, int &ch, int &i, int &unit) {
+        const int seg = st / n_uni;
+        i = st % n_uni;
+        ch = seg % chunks;
+        tile0 = ((int)blockIdx.x + (seg / chunks) * (int)gridDim.x) * RT;
+        const int in_chunk = min(upc, units - ch * upc);
+        const int lu = min(wave + i * GW, in_chunk - 1);
+        unit = ch * upc + lu;
+    };
     typedef typename std::conditional<BITS == 8, u32x4, uint2>::type Raw;
+    typedef typename std::conditional<sizeof(ST) == 4, floatx4, uint2>::type SRaw;
     Raw ring[PFU][RT][UW];
-    auto load_unit = [&](int i, Raw (&dst)[RT][UW]) {
-        const int u = wave + i * GW;
+    SRaw sring[PFU][RT];
+    auto load_step = [&](int st, Raw (&dst)[RT][UW], SRaw (&sdst)[RT]) {
+        int tile0, ch, i, u;
+        step_unit(st, tile0, ch, i, u);
+        const int gi = (u * UC) / group;
 #pragma unroll
-        for (int r = 0; r < RT; ++r)
+        for (int r = 0; r < RT; ++r) {
+            const uint8_t *rowp = codes + (size_t)((tile0 + r) * 16 + c) * row_bytes + CB * q;
 #pragma unroll
             for (int w = 0; w < UW; ++w) {
                 const size_t off = (size_t)(u * UW + w) * (BITS == 8 ? 64 : 32);
                 if constexpr (BITS == 8)
-                    dst[r][w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(arow[r] + off));
+                    dst[r][w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(rowp + off));
                 else
-                    dst[r][w] = *reinterpret_cast<const uint2 *>(arow[r] + off);
+                    dst[r][w] = *reinterpret_cast<const uint2 *>(rowp + off);
             }
+            sdst[r] = *reinterpret_cast<const SRaw *>(scales + ((size_t)(tile0 + r) * groups + gi) * 16 + 4 * q);
+        }
     };
+    const int last_s = total_s > 0 ? total_s - 1 : 0;
+    if (total_s > 0) {
 #pragma unroll
-    for (int j = 0; j < PFU; ++j) load_unit(min(j, last), ring[j]);
-
-    // ---- scales of the tile
-    {
-        const int words = (int)(sc_bytes / 16);
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(scales + (size_t)tile0 * groups * 16);
-        for (int i = threadIdx.x; i < words; i += 64 * GW) reinterpret_cast<u32x4 *>(sc_l)[i] = src[i];
+        for (int j = 0; j < PFU; ++j) load_step(min(j, last_s), ring[j], sring[j]);
     }
 
     // ---- per-token statistics: RMSNorm factor and the power of two for the limbs
@@ -188,16 +205,10 @@ __global__ __launch_bounds__(64 * GW) void gemv_q(const uint8_t *__restrict__ co
     }
     __syncthreads();
 
-    floatx4 total[RT][1];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) total[r][0] = (floatx4){0.f, 0.f, 0.f, 0.f};
-
-    const int chunks = (cols + kc - 1) / kc;
-    const int upc = kc / UC;  // units per chunk
-    for (int ch = 0; ch < chunks; ++ch) {
+    // ---- limbs of chunk ch into LDS: a thread takes 8 consecutive columns of one token
+    auto stage = [&](int ch) {
         const int col0 = ch * kc;
         const int kcols = min(kc, cols - col0);
-        // ---- limbs of this chunk: thread takes 8 consecutive columns of one token
         for (int idx = threadIdx.x; idx < tokens * (kcols / 8); idx += 64 * GW) {
             const int t = idx / (kcols / 8), k8 = (idx % (kcols / 8)) * 8;
             const TokenStat st = stat[t];
@@ -228,146 +239,159 @@ __global__ __launch_bounds__(64 * GW) void gemv_q(const uint8_t *__restrict__ co
                 *reinterpret_cast<uint2 *>(limbs + (size_t)(t * LIMBS + l) * kc + k8) =
                     make_uint2(packed[l][0], packed[l][1]);
             if constexpr (BITS == 4) {
-                // per-unit column sums: UC/8 threads share a unit (consecutive idx, aligned groups)
+                // per-unit column sums: UC/8 consecutive threads share a unit
 #pragma unroll
                 for (int l = 0; l < LIMBS; ++l) {
-                    int s = 0;
+                    int sum = 0;
 #pragma unroll
                     for (int h = 0; h < 2; ++h)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) s += (int)(int8_t)((packed[l][h] >> (8 * e)) & 0xffu);
+                        for (int e = 0; e < 4; ++e) sum += (int)(int8_t)((packed[l][h] >> (8 * e)) & 0xffu);
 #pragma unroll
-                    for (int o = 1; o < UC / 8; o <<= 1) s += __shfl_xor(s, o);
-                    if ((idx % (UC / 8)) == 0) colsum[(k8 / UC) * 16 + t * LIMBS + l] = s;
+                    for (int o = 1; o < UC / 8; o <<= 1) sum += __shfl_xor(sum, o);
+                    if ((idx % (UC / 8)) == 0) colsum[(k8 / UC) * 16 + t * LIMBS + l] = sum;
                 }
             }
         }
+    };
+    if (chunks == 1) {
+        stage(0);
         __syncthreads();
+    }
 
-        // ---- this wave's units in the chunk: i in [i0, i1)
-        const int u_begin = ch * upc, u_end = min(units, u_begin + upc);
-        const int i0 = u_begin > wave ? (u_begin - wave + GW - 1) / GW : 0;
-        const int i1 = u_end > wave ? (u_end - wave + GW - 1) / GW : 0;
-        for (int base = i0; base < i1; base += PFU) {
+    floatx4 total[RT];
 #pragma unroll
-            for (int j = 0; j < PFU; ++j) {
-                // i0 is a multiple of PFU (chunks hold a multiple of GW * PFU units), so slot j holds unit i
-                const int i = base + j;
-                Raw cur[RT][UW];
+    for (int r = 0; r < RT; ++r) total[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    unsigned long long best = 0;  // greedy choice over this block's rows (argmax mode)
+
+    for (int base = 0; base < total_s; base += PFU) {
 #pragma unroll
-                for (int r = 0; r < RT; ++r)
+        for (int j = 0; j < PFU; ++j) {
+            const int st = base + j;  // slot j holds step st (base is a multiple of PFU)
+            if (st >= total_s) break;
+            Raw cur[RT][UW];
+            SRaw scur[RT];
 #pragma unroll
-                    for (int w = 0; w < UW; ++w) cur[r][w] = ring[j][r][w];
-                // refill the slot with the unit PFU ahead (re-reading the last one past the end)
-                load_unit(min(i + PFU, last), ring[j]);
-                if (i < i1) {
-                    const int u = wave + i * GW;
-                    const int lcol = u * UC - col0;  // column of the unit inside the chunk
-                    int4v b[UW];
+            for (int r = 0; r < RT; ++r) {
+                scur[r] = sring[j][r];
+#pragma unroll
+                for (int w = 0; w < UW; ++w) cur[r][w] = ring[j][r][w];
+            }
+            load_step(min(st + PFU, last_s), ring[j], sring[j]);
+            int tile0, ch, i, u;
+            step_unit(st, tile0, ch, i, u);
+            if (chunks > 1 && i == 0) {
+                __syncthreads();
+                stage(ch);
+                __syncthreads();
+            }
+            const int in_chunk = min(upc, units - ch * upc);
+            if (wave + i * GW < in_chunk) {
+                const int lcol = u * UC - ch * kc;  // column of the unit inside the chunk
+                int4v b[UW];
+#pragma unroll
+                for (int w = 0; w < UW; ++w) {
+                    b[w] = (int4v){0, 0, 0, 0};
+                    if (c < used)
+                        b[w] = *reinterpret_cast<const int4v *>(limbs + (size_t)c * kc + lcol + 64 * w + 16 * q);
+                }
+                int csum = 0;
+                if constexpr (BITS == 4) csum = c < used ? colsum[(lcol / UC) * 16 + c] : 0;
+#pragma unroll
+                for (int r = 0; r < RT; ++r) {
+                    int4v acc = (int4v){0, 0, 0, 0};
 #pragma unroll
                     for (int w = 0; w < UW; ++w) {
-                        b[w] = (int4v){0, 0, 0, 0};
-                        if (c < used)
-                            b[w] = *reinterpret_cast<const int4v *>(limbs + (size_t)c * kc + lcol + 64 * w + 16 * q);
-                    }
-                    int csum = 0;
-                    if constexpr (BITS == 4) csum = c < used ? colsum[(lcol / UC) * 16 + c] : 0;
-                    const int gi = (u * UC) / group;
-#pragma unroll
-                    for (int r = 0; r < RT; ++r) {
-                        int4v acc = (int4v){0, 0, 0, 0};
-#pragma unroll
-                        for (int w = 0; w < UW; ++w) {
-                            int4v a;
-                            const Raw raw = cur[r][w];
-                            if constexpr (BITS == 8) {
-                                a = __builtin_bit_cast(int4v, raw);
-                            } else {
-                                a = (int4v){(int)(raw.x & 0x0f0f0f0fu), (int)((raw.x >> 4) & 0x0f0f0f0fu),
-                                            (int)(raw.y & 0x0f0f0f0fu), (int)((raw.y >> 4) & 0x0f0f0f0fu)};
-                            }
-                            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[w], acc, 0, 0, 0);
+                        int4v a;
+                        if constexpr (BITS == 8) {
+                            a = __builtin_bit_cast(int4v, cur[r][w]);
+                        } else {
+                            const uint2 raw = cur[r][w];
+                            a = (int4v){(int)(raw.x & 0x0f0f0f0fu), (int)((raw.x >> 4) & 0x0f0f0f0fu),
+                                        (int)(raw.y & 0x0f0f0f0fu), (int)((raw.y >> 4) & 0x0f0f0f0fu)};
                         }
-                        if constexpr (BITS == 4) acc -= (int4v){8 * csum, 8 * csum, 8 * csum, 8 * csum};
-                        const ST *sp = sc_l + ((size_t)r * groups + gi) * 16 + 4 * q;
-                        floatx4 s;
-                        if constexpr (sizeof(ST) == 4) s = *reinterpret_cast<const floatx4 *>(sp);
-                        else s = (floatx4){scale_at(sp), scale_at(sp + 1), scale_at(sp + 2), scale_at(sp + 3)};
-                        const floatx4 d = (floatx4){(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
-                        total[r][0] += d * s;
+                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[w], acc, 0, 0, 0);
                     }
+                    if constexpr (BITS == 4) acc -= (int4v){8 * csum, 8 * csum, 8 * csum, 8 * csum};
+                    floatx4 sv;
+                    if constexpr (sizeof(ST) == 4) {
+                        sv = scur[r];
+                    } else {
+                        const uint2 sr = scur[r];
+                        sv = (floatx4){__uint_as_float(sr.x << 16), __uint_as_float(sr.x & 0xffff0000u),
+                                       __uint_as_float(sr.y << 16), __uint_as_float(sr.y & 0xffff0000u)};
+                    }
+                    const floatx4 d = (floatx4){(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
+                    total[r] += d * sv;
                 }
             }
-        }
-        __syncthreads();
-    }
-
-    // ---- reduce: red[wave][tile][column][row] (reuses the limb area), then limbs, waves and the limb weights
-    float *red = reinterpret_cast<float *>(limbs);
-    float *vals = red + GW * RT * 16 * 16;
-    if (c < used) {
+            if (i == n_uni - 1 && ch == chunks - 1) {
+                // ---- end of a tile block: sum the waves and limbs, then the epilogue
+                if (c < used) {
 #pragma unroll
-        for (int r = 0; r < RT; ++r)
+                    for (int r = 0; r < RT; ++r)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) red[((wave * RT + r) * 16 + c) * 16 + 4 * q + k] = total[r][0][k];
-    }
-    __syncthreads();
-    const int outputs = RT * tokens * 16;
-    for (int o = threadIdx.x; o < outputs; o += 64 * GW) {
-        const int r = o / (tokens * 16), t = (o / 16) % tokens, row = o % 16;
-        float v = 0.0f;
-        float lw = stat[t].down;
+                        for (int k = 0; k < 4; ++k) red[((wave * RT + r) * 16 + c) * 16 + 4 * q + k] = total[r][k];
+                }
 #pragma unroll
-        for (int l = 0; l < LIMBS; ++l) {
-            float part = 0.0f;
+                for (int r = 0; r < RT; ++r) total[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+                __syncthreads();
+                const int outputs = RT * tokens * 16;
+                for (int o = threadIdx.x; o < outputs; o += 64 * GW) {
+                    const int r = o / (tokens * 16), t = (o / 16) % tokens, row = o % 16;
+                    float v = 0.0f;
+                    float lw = stat[t].down;
 #pragma unroll
-            for (int wv = 0; wv < GW; ++wv) part += red[((wv * RT + r) * 16 + t * LIMBS + l) * 16 + row];
-            v += part * lw;
-            lw *= 256.0f;
-        }
-        vals[(r * GEMV_TOKENS + t) * 16 + row] = v;
-    }
-    __syncthreads();
-
-    if (out.mode == OUT_SILU) {
-        const int pairs = RT * 8 * tokens;
-        for (int o = threadIdx.x; o < pairs; o += 64 * GW) {
-            const int r = o / (tokens * 8), t = (o / 8) % tokens, pr = o % 8;
-            const int row = (tile0 + r) * 16 + 2 * pr;
-            if (row >= rows) continue;
-            const float g = vals[(r * GEMV_TOKENS + t) * 16 + 2 * pr];
-            const float u = vals[(r * GEMV_TOKENS + t) * 16 + 2 * pr + 1];
-            reinterpret_cast<float *>(out.y)[(size_t)t * out.y_stride + (row >> 1)] = silu_f(g) * u;
-        }
-        return;
-    }
-    for (int o = threadIdx.x; o < outputs; o += 64 * GW) {
-        const int r = o / (tokens * 16), t = (o / 16) % tokens, row16 = o % 16;
-        const int row = (tile0 + r) * 16 + row16;
-        if (row >= rows) continue;
-        const float v = vals[(r * GEMV_TOKENS + t) * 16 + row16];
-        const size_t at = (size_t)t * out.y_stride + row;
-        if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v;
-        else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v;
-        else {
-            const unsigned uu = __float_as_uint(v);
-            reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
-                (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+                    for (int l = 0; l < LIMBS; ++l) {
+                        float part = 0.0f;
+#pragma unroll
+                        for (int wv = 0; wv < GW; ++wv) part += red[((wv * RT + r) * 16 + t * LIMBS + l) * 16 + row];
+                        v += part * lw;
+                        lw *= 256.0f;
+                    }
+                    vals[(r * GEMV_TOKENS + t) * 16 + row] = v;
+                }
+                __syncthreads();
+                if (out.mode == OUT_SILU) {
+                    const int pairs = RT * 8 * tokens;
+                    for (int o = threadIdx.x; o < pairs; o += 64 * GW) {
+                        const int r = o / (tokens * 8), t = (o / 8) % tokens, pr = o % 8;
+                        const int row = (tile0 + r) * 16 + 2 * pr;
+                        if (row >= rows) continue;
+                        const float g = vals[(r * GEMV_TOKENS + t) * 16 + 2 * pr];
+                        const float uu = vals[(r * GEMV_TOKENS + t) * 16 + 2 * pr + 1];
+                        reinterpret_cast<float *>(out.y)[(size_t)t * out.y_stride + (row >> 1)] = silu_f(g) * uu;
+                    }
+                } else {
+                    for (int o = threadIdx.x; o < outputs; o += 64 * GW) {
+                        const int r = o / (tokens * 16), t = (o / 16) % tokens, row16 = o % 16;
+                        const int row = (tile0 + r) * 16 + row16;
+                        if (row >= rows) continue;
+                        const float v = vals[(r * GEMV_TOKENS + t) * 16 + row16];
+                        const size_t at = (size_t)t * out.y_stride + row;
+                        if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v;
+                        else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v;
+                        else {
+                            const unsigned uu = __float_as_uint(v);
+                            reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
+                                (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
+                                                                 : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+                        }
+                        if (out.argmax && t == tokens - 1) {
+                            // largest under f32's total order, lowest row on ties (sampler/src/lib.rs:40-48)
+                            const unsigned long long key =
+                                (unsigned long long)((unsigned)total_key(v) ^ 0x80000000u) << 32 |
+                                (unsigned long long)(0xffffffffu - (unsigned)row);
+                            best = key > best ? key : best;
+                        }
+                    }
+                }
+                // vals/red are rewritten by the next tile block only after every thread has read them
+                __syncthreads();
+            }
         }
     }
     if (out.argmax) {
-        // greedy choice of the last token: the largest under f32's total order, the lowest row on ties
-        // (sampler/src/lib.rs:40-48). One 64-bit atomic max per block on (key, ~row).
-        unsigned long long best = 0;
-        const int t = tokens - 1;
-        for (int o = threadIdx.x; o < RT * 16; o += 64 * GW) {
-            const int row = (tile0 + o / 16) * 16 + o % 16;
-            if (row >= rows) continue;
-            const float v = vals[((o / 16) * GEMV_TOKENS + t) * 16 + o % 16];
-            const unsigned long long key = (unsigned long long)((unsigned)total_key(v) ^ 0x80000000u) << 32 |
-                                           (unsigned long long)(0xffffffffu - (unsigned)row);
-            best = key > best ? key : best;
-        }
         for (int o = 32; o > 0; o >>= 1) {
             const unsigned long long other = __shfl_xor(best, o);
             best = other > best ? other : best;
@@ -385,11 +409,12 @@ static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in
     const size_t groups = w->groups();
     // the whole row of limbs when it fits, else chunks of 4096 columns (a multiple of GW * pfu(RT) units)
     const size_t kc = tokens * LIMBS * w->cols <= (size_t)LDS_LIMBS ? w->cols : 4096;
-    const size_t sc_bytes = ((size_t)RT * groups * 16 * sizeof(ST) + 15) & ~size_t(15);
-    const size_t limb_bytes = std::max(tokens * LIMBS * kc + (BITS == 4 ? (kc / (64 * UW)) * 16 * 4 : 0),
-                                       (size_t)(GW * RT * 16 * 16 + RT * GEMV_TOKENS * 16) * 4);
-    const size_t lds = 256 + sc_bytes + limb_bytes;
-    dim3 grid((unsigned)(w->rows_padded / 16 / RT));
+    (void)groups;
+    const size_t lds = 256 + tokens * LIMBS * kc + (BITS == 4 ? (kc / (64 * UW)) * 16 * 4 : 0) +
+                       (size_t)(GW * RT * 16 * 16 + RT * GEMV_TOKENS * 16) * 4;
+    // Persistent when the limbs stay in LDS for the whole launch: two blocks per compute unit walk the tile blocks.
+    const size_t tile_blocks = w->rows_padded / 16 / RT;
+    const size_t cu = (size_t)std::max(g->cu_count, 1);
     auto kern1 = gemv_q<BITS, RT, UW, ST, true>;
     auto kernn = gemv_q<BITS, RT, UW, ST, false>;
     auto kern = tokens == 1 ? kern1 : kernn;
@@ -397,16 +422,21 @@ static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in
         if (lds > 160 * 1024) unsupported("gemv shared memory (KiB)", 160, lds / 1024);
         HIP_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     }
+    int resident = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * GW, lds) != hipSuccess || resident < 1)
+        resident = 1;
+    const size_t blocks = kc == w->cols ? std::min(tile_blocks, (size_t)resident * cu) : tile_blocks;
+    dim3 grid((unsigned)blocks);
     kern<<<grid, dim3(64 * GW), lds, g->stream>>>(w->codes, (const ST *)w->scales, in, out, (int)tokens,
-                                                   (int)w->rows, (int)w->cols, (int)w->group, (int)kc);
+                                                   (int)w->rows, (int)w->cols, (int)w->group, (int)kc,
+                                                   (int)tile_blocks);
 }
 
 template <int BITS, int UW, typename ST>
 static void launch_rt(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     const size_t tiles = w->rows_padded / 16;
-    if (tiles >= 4096) launch_t<BITS, 4, UW, ST>(g, w, in, out, tokens);
-    else if (tiles >= 2048) launch_t<BITS, 2, UW, ST>(g, w, in, out, tokens);
-    else launch_t<BITS, 1, UW, ST>(g, w, in, out, tokens);
+    (void)tiles;
+    launch_t<BITS, 1, UW, ST>(g, w, in, out, tokens);
 }
 
 template <typename ST>
