@@ -19,7 +19,8 @@ size_t kv_elem_bytes(marin_kv_format f) { return f == MARIN_KV_F32 ? 4 : 2; }
 
 constexpr int ROWS = 8;         // query rows per workgroup
 constexpr int MAX_CHUNK = 256;  // positions per workgroup
-constexpr int MIN_CHUNK = 32;
+constexpr int MIN_CHUNK = 64;
+constexpr int UNR = 8;  // position steps whose rows are loaded before any is used
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
@@ -70,8 +71,10 @@ __device__ __forceinline__ const uint8_t *kv_row(const uint64_t *table, const Kv
                                              (uint64_t)kvh * g.head_bytes + (uint64_t)in_page * g.head_dim * es);
 }
 
-// grid: x = chunk (split), y = kv_head * row_groups + row_group, z = sequence. LPP lanes per position.
-template <int F, int LPP, bool VEC, bool QBF16>
+// grid: x = chunk (split), y = kv_head * row_groups + row_group, z = sequence. LPP lanes per position, R query rows
+// (the heads of one kv head times the new tokens, in groups of R). The chunk's page addresses are read into LDS
+// first, so every row address is computed without another memory round trip.
+template <int F, int LPP, bool VEC, bool QBF16, int R>
 __global__ __launch_bounds__(256) void attention_partial(const void *__restrict__ qv, const uint64_t *__restrict__ tables,
                                                          size_t table_stride, const uint32_t *__restrict__ ctx_lens,
                                                          KvGeom geom, int tokens, int heads, int kv_heads, int chunk,
@@ -82,27 +85,35 @@ __global__ __launch_bounds__(256) void attention_partial(const void *__restrict_
     const int hd = (int)geom.head_dim;
     const int group = heads / kv_heads;
     const int total_rows = tokens * group;
-    const int row_groups = (total_rows + ROWS - 1) / ROWS;
+    const int row_groups = (total_rows + R - 1) / R;
     const int kvh = blockIdx.y / row_groups, rg = blockIdx.y % row_groups;
     const int b = blockIdx.z, split = blockIdx.x;
     const int ctx = (int)ctx_lens[b];
     const int first = split * chunk;
     if (first >= ctx) return;
     const int count = min(chunk, ctx - first);
-    const int r0 = rg * ROWS;
-    const int nrows = min(ROWS, total_rows - r0);
+    const int r0 = rg * R;
+    const int nrows = min(R, total_rows - r0);
     const uint64_t *table = tables + (size_t)b * table_stride;
     const int d = sub * 8;
+    const size_t es = F == MARIN_KV_F32 ? 4 : 2;
+    const uint64_t head_off = (uint64_t)kvh * geom.head_bytes + geom.layer_offset;
+    const uint32_t pmask = (1u << geom.page_shift) - 1u;
 
-    __shared__ float w_s[ROWS][MAX_CHUNK];
-    __shared__ float red[4][ROWS][8 * 32];  // wave partial accumulators (only head_dim used)
-    __shared__ float ml_s[ROWS][2];
+    __shared__ float w_s[R][MAX_CHUNK];
+    __shared__ float red[4][R][8 * 32];  // wave partial accumulators (only head_dim used)
+    __shared__ float ml_s[R][2];
+    __shared__ uint64_t pages_s[MAX_CHUNK + 1];
+
+    const int page0 = first >> geom.page_shift;
+    const int npages = ((first + count - 1) >> geom.page_shift) - page0 + 1;
+    for (int i = threadIdx.x; i < npages; i += 256) pages_s[i] = table[page0 + i] + head_off;
 
     // Query rows: row r = (token r / group, head kvh * group + r % group).
-    float q[ROWS][8];
-    int visible[ROWS];
+    float q[R][8];
+    int visible[R];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int rr = r0 + r;
         const int t = rr / group, h = kvh * group + rr % group;
         visible[r] = ctx - tokens + t + 1;
@@ -119,21 +130,36 @@ __global__ __launch_bounds__(256) void attention_partial(const void *__restrict_
             }
         }
     }
+    __syncthreads();
+    auto row_ptr = [&](int which, int p) {
+        const uint32_t pos = (uint32_t)(first + p);
+        return reinterpret_cast<const uint8_t *>(pages_s[(pos >> geom.page_shift) - page0] +
+                                                 (which ? geom.value_offset : 0) + (uint64_t)(pos & pmask) * hd * es);
+    };
 
-    // Scores.
-    for (int p0 = wave * PPW; p0 < count; p0 += 4 * PPW) {
-        const int p = p0 + slot;
-        float k[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (p < count && d < hd) load8<F, VEC>(kv_row(table, geom, 0, kvh, (uint32_t)(first + p)), d, hd, k);
+    // Scores: UNR rows per lane group are loaded before the dots, so each wave keeps UNR * 16 bytes per lane in flight.
+    for (int p0 = wave * PPW; p0 < count; p0 += 4 * PPW * UNR) {
+        float k[UNR][8];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            float s = 0.0f;
+        for (int u = 0; u < UNR; ++u) {
+            const int p = p0 + u * 4 * PPW + slot;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s += q[r][i] * k[i];
+            for (int i = 0; i < 8; ++i) k[u][i] = 0.0f;
+            if (p < count && d < hd) load8<F, VEC>(row_ptr(0, p), d, hd, k[u]);
+        }
 #pragma unroll
-            for (int o = 1; o < LPP; o <<= 1) s += __shfl_xor(s, o);
-            if (sub == 0 && p < count && r < nrows)
-                w_s[r][p] = (first + p < visible[r]) ? s * scale : -INFINITY;
+        for (int u = 0; u < UNR; ++u) {
+            const int p = p0 + u * 4 * PPW + slot;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sc += q[r][i] * k[u][i];
+#pragma unroll
+                for (int o = 1; o < LPP; o <<= 1) sc += __shfl_xor(sc, o);
+                if (sub == 0 && p < count && r < nrows)
+                    w_s[r][p] = (first + p < visible[r]) ? sc * scale : -INFINITY;
+            }
         }
     }
     __syncthreads();
@@ -158,34 +184,43 @@ __global__ __launch_bounds__(256) void attention_partial(const void *__restrict_
     __syncthreads();
 
     // Weighted values.
-    float acc[ROWS][8];
+    float acc[R][8];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[r][i] = 0.0f;
-    for (int p0 = wave * PPW; p0 < count; p0 += 4 * PPW) {
-        const int p = p0 + slot;
-        if (p < count && d < hd) {
-            float v[8];
-            load8<F, VEC>(kv_row(table, geom, 1, kvh, (uint32_t)(first + p)), d, hd, v);
+    for (int p0 = wave * PPW; p0 < count; p0 += 4 * PPW * UNR) {
+        float v[UNR][8];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const float wgt = w_s[r][p];
+        for (int u = 0; u < UNR; ++u) {
+            const int p = p0 + u * 4 * PPW + slot;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[r][i] += wgt * v[i];
+            for (int i = 0; i < 8; ++i) v[u][i] = 0.0f;
+            if (p < count && d < hd) load8<F, VEC>(row_ptr(1, p), d, hd, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int p = p0 + u * 4 * PPW + slot;
+            if (p < count) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float wgt = w_s[r][p];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[r][i] += wgt * v[u][i];
+                }
             }
         }
     }
     // Reduce over the position slots of the wave (lanes with the same sub), then over the waves.
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int o = LPP; o < 64; o <<= 1) acc[r][i] += __shfl_xor(acc[r][i], o);
     if (slot == 0 && d < hd) {
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 if (d + i < 8 * 32) red[wave][r][d + i] = acc[r][i];
@@ -205,26 +240,35 @@ __global__ __launch_bounds__(256) void attention_partial(const void *__restrict_
     }
 }
 
-// Combines the chunks of one (sequence, token, head): out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
+// Combines the chunks of one (sequence, token, head): out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}. The
+// chunks' weights e^{m_s - M} are computed once into LDS, then each thread sums one element over the chunks.
 template <int OUT>
-__global__ void attention_merge(const float *__restrict__ part, const uint32_t *__restrict__ ctx_lens, int tokens,
-                                int heads, int hd, int chunk, int splits, void *__restrict__ out,
-                                float *__restrict__ split_inv) {
+__global__ __launch_bounds__(256) void attention_merge(const float *__restrict__ part,
+                                                       const uint32_t *__restrict__ ctx_lens, int tokens, int heads,
+                                                       int hd, int chunk, int splits, void *__restrict__ out) {
+    extern __shared__ float ws[];  // [splits] weights, then the total
     const int unit = blockIdx.x;  // (b * tokens + t) * heads + h
     const int b = unit / (tokens * heads);
     const int used = min(splits, (int)((ctx_lens[b] + chunk - 1) / chunk));
     const float *p = part + (size_t)unit * splits * (hd + 2);
+    __shared__ float red[4];
     float m = -INFINITY;
-    for (int s = 0; s < used; ++s) m = fmaxf(m, p[(size_t)s * (hd + 2)]);
+    for (int s = threadIdx.x; s < used; s += blockDim.x) m = fmaxf(m, p[(size_t)s * (hd + 2)]);
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = fmaxf(m, red[w]);
+    for (int s = threadIdx.x; s < used; s += blockDim.x) {
+        const float ms = p[(size_t)s * (hd + 2)];
+        ws[s] = ms == -INFINITY ? 0.0f : expf(ms - m);
+    }
+    __syncthreads();
+    float total = 0.0f;
+    for (int s = 0; s < used; ++s) total += p[(size_t)s * (hd + 2) + 1] * ws[s];
     for (int e = threadIdx.x; e < hd; e += blockDim.x) {
-        float total = 0.0f, acc = 0.0f;
-        for (int s = 0; s < used; ++s) {
-            const float ms = p[(size_t)s * (hd + 2)];
-            if (ms == -INFINITY) continue;
-            const float f = expf(ms - m);
-            total += p[(size_t)s * (hd + 2) + 1] * f;
-            acc += p[(size_t)s * (hd + 2) + 2 + e] * f;
-        }
+        float acc = 0.0f;
+        for (int s = 0; s < used; ++s) acc += p[(size_t)s * (hd + 2) + 2 + e] * ws[s];
         const float v = acc / total;
         const size_t at = (size_t)unit * hd + e;
         if constexpr (OUT == 0) reinterpret_cast<float *>(out)[at] = v;
@@ -232,23 +276,12 @@ __global__ void attention_merge(const float *__restrict__ part, const uint32_t *
             const unsigned u = __float_as_uint(v);
             reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
         }
-        if constexpr (OUT == 2) {
-            // f16 hi/lo split for the output projection: [token][2][heads * hd]
-            const int t = (unit / heads) % tokens, h = unit % heads;
-            const size_t width = (size_t)heads * hd;
-            _Float16 *d = reinterpret_cast<_Float16 *>(out);
-            const _Float16 hi = (_Float16)v;
-            d[((size_t)t * 2) * width + (size_t)h * hd + e] = hi;
-            d[((size_t)t * 2 + 1) * width + (size_t)h * hd + e] = (_Float16)(v - (float)hi);
-        }
-    }
-    if constexpr (OUT == 2) {
-        if (unit % heads == 0 && threadIdx.x == 0) split_inv[(unit / heads) % tokens] = 1.0f;
     }
 }
 
+// Positions per workgroup: enough workgroups for about two per compute unit, 64 to 256 positions each.
 static int chunk_for(size_t max_ctx, size_t blocks_per_chunk, int cu_count) {
-    const size_t wanted = std::max<size_t>(1, (4 * (size_t)std::max(cu_count, 1) + blocks_per_chunk - 1) /
+    const size_t wanted = std::max<size_t>(1, (2 * (size_t)std::max(cu_count, 1) + blocks_per_chunk - 1) /
                                                   std::max<size_t>(blocks_per_chunk, 1));
     size_t chunk = (max_ctx + wanted - 1) / wanted;
     chunk = std::min<size_t>(MAX_CHUNK, std::max<size_t>(MIN_CHUNK, chunk));
@@ -262,16 +295,29 @@ size_t attention_partial_floats(size_t batch, size_t tokens, size_t heads, size_
     return batch * tokens * heads * std::max<size_t>(splits, 1) * (head_dim + 2);
 }
 
-template <int F, int LPP, bool VEC>
-static void launch_partial(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+template <int F, int LPP, bool VEC, int R>
+static void launch_partial_r(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
     if (a.q_bf16)
-        attention_partial<F, LPP, VEC, true><<<grid, dim3(256), 0, g->stream>>>(
+        attention_partial<F, LPP, VEC, true, R><<<grid, dim3(256), 0, g->stream>>>(
             a.q, a.tables, a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk, splits,
             scale, a.partials);
     else
-        attention_partial<F, LPP, VEC, false><<<grid, dim3(256), 0, g->stream>>>(
+        attention_partial<F, LPP, VEC, false, R><<<grid, dim3(256), 0, g->stream>>>(
             a.q, a.tables, a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk, splits,
             scale, a.partials);
+}
+
+static int rows_per_block(const AttentionArgs &a) {
+    const size_t rows = a.tokens * (a.heads / a.kv_heads);
+    return rows <= 2 ? 2 : (rows <= 4 ? 4 : ROWS);
+}
+
+template <int F, int LPP, bool VEC>
+static void launch_partial(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    const int r = rows_per_block(a);
+    if (r == 2) launch_partial_r<F, LPP, VEC, 2>(g, a, grid, chunk, splits, scale);
+    else if (r == 4) launch_partial_r<F, LPP, VEC, 4>(g, a, grid, chunk, splits, scale);
+    else launch_partial_r<F, LPP, VEC, ROWS>(g, a, grid, chunk, splits, scale);
 }
 
 template <int F>
@@ -298,7 +344,8 @@ static void launch_partial_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, in
 
 void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     const size_t group = a.heads / a.kv_heads;
-    const size_t row_groups = (a.tokens * group + ROWS - 1) / ROWS;
+    const size_t rpb = (size_t)rows_per_block(a);
+    const size_t row_groups = (a.tokens * group + rpb - 1) / rpb;
     const int chunk = chunk_for(a.max_ctx, a.kv_heads * row_groups * a.batch, g->cu_count);
     const int splits = (int)((a.max_ctx + chunk - 1) / chunk);
     if ((size_t)splits * a.batch * a.tokens * a.heads * (a.geom.head_dim + 2) > a.partial_floats)
@@ -314,15 +361,13 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     g->launched(marin_gpu::ATTENTION, a.bytes_hint);
     const dim3 mgrid((unsigned)(a.batch * a.tokens * a.heads));
     const dim3 mblock((unsigned)std::min<size_t>(256, (a.geom.head_dim + 63) / 64 * 64));
+    const size_t mlds = (size_t)splits * 4;
     if (a.out_kind == 0)
-        attention_merge<0><<<mgrid, mblock, 0, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
-                                                            (int)a.geom.head_dim, chunk, splits, a.out, nullptr);
-    else if (a.out_kind == 1)
-        attention_merge<1><<<mgrid, mblock, 0, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
-                                                            (int)a.geom.head_dim, chunk, splits, a.out, nullptr);
+        attention_merge<0><<<mgrid, mblock, mlds, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
+                                                               (int)a.geom.head_dim, chunk, splits, a.out);
     else
-        attention_merge<2><<<mgrid, mblock, 0, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
-                                                            (int)a.geom.head_dim, chunk, splits, a.out, a.split_inv);
+        attention_merge<1><<<mgrid, mblock, mlds, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
+                                                               (int)a.geom.head_dim, chunk, splits, a.out);
     g->launched(marin_gpu::ATTENTION, 0.0);
 }
 
@@ -599,6 +644,8 @@ struct marin_page_pool {
     size_t ctx_cap = 0;
     float *partials = nullptr;
     size_t partial_floats = 0;
+    std::vector<uint64_t> last_tables;  // what the device copies hold, to skip unchanged uploads
+    std::vector<uint32_t> last_ctx;
 };
 
 extern "C" {
@@ -675,12 +722,14 @@ marin_status marin_paged_attention_batch(marin_gpu *g, const marin_buffer *q, ma
             p->tables = nullptr;
             p->tables = (uint64_t *)g->alloc(addr.size() * 8, false);
             p->table_cap = addr.size();
+            p->last_tables.clear();
         }
         if (batch > p->ctx_cap) {
             g->release(p->ctx);
             p->ctx = nullptr;
             p->ctx = (uint32_t *)g->alloc(batch * 4, false);
             p->ctx_cap = batch;
+            p->last_ctx.clear();
         }
         const size_t need_partials = attention_partial_floats(batch, 1, heads, hd, max_ctx, g->cu_count);
         if (need_partials > p->partial_floats) {
@@ -689,8 +738,15 @@ marin_status marin_paged_attention_batch(marin_gpu *g, const marin_buffer *q, ma
             p->partials = (float *)g->alloc(need_partials * 4, false);
             p->partial_floats = need_partials;
         }
-        g->upload(p->tables, addr.data(), addr.size() * 8);
-        g->upload(p->ctx, ctx_lens, batch * 4);
+        if (p->last_tables != addr) {
+            g->upload(p->tables, addr.data(), addr.size() * 8);
+            p->last_tables = addr;
+        }
+        std::vector<uint32_t> ctxv(ctx_lens, ctx_lens + batch);
+        if (p->last_ctx != ctxv) {
+            g->upload(p->ctx, ctx_lens, batch * 4);
+            p->last_ctx = ctxv;
+        }
         AttentionArgs a{};
         a.q = q->data;
         a.q_bf16 = true;

@@ -64,7 +64,7 @@ struct AttentionArgs {
     const void *q;
     bool q_bf16;
     void *out;
-    int out_kind;  // 0 f32, 1 bf16, 2 f16 split (parts hi/lo, [t][2][heads*head_dim], inv = 1)
+    int out_kind;  // 0 f32, 1 bf16
     const uint64_t *tables;
     size_t table_stride;
     const uint32_t *ctx;  // device
@@ -73,7 +73,6 @@ struct AttentionArgs {
     size_t max_ctx;  // bound on every ctx[b], sets the grid
     float *partials;
     size_t partial_floats;
-    float *split_inv;  // out_kind 2: where the per-token inverse scale goes
     double bytes_hint = 0.0;  // algorithmic bytes, for launch accounting only
 };
 size_t attention_partial_floats(size_t batch, size_t tokens, size_t heads, size_t head_dim, size_t max_ctx,
