@@ -8,7 +8,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmarin_hip.so")
+# MARIN_HIP_LIB names another build of the library (a variant under test); the in-tree build otherwise.
+LIB_PATH = os.environ.get("MARIN_HIP_LIB") or os.path.join(HERE, "libmarin_hip.so")
 
 P = C.c_void_p
 PP = C.POINTER(C.c_void_p)

@@ -4,8 +4,9 @@
 // Attention splits the visible context into chunks; a workgroup takes one chunk of one kv head for up to 8 query rows
 // (the heads sharing that kv head, times the new tokens). Lanes are grouped per position: a group of LPP lanes covers
 // one position's head with 8 contiguous values per lane (16-byte loads for bf16/f16), so a wave reads 64/LPP rows of
-// a page per step and each key or value row is read once for all the rows of the group. Scores go to LDS; each chunk
-// leaves its maximum, sum of weights and weighted values, and a merge kernel combines the chunks (log-sum-exp).
+// a page per step and each key or value row is read once for all the rows of the group. Keys and values are read in
+// the same pass with an online softmax; the chunks of a row group are merged (log-sum-exp) by the last of them to
+// finish, in the same launch.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -19,47 +20,76 @@ size_t kv_elem_bytes(marin_kv_format f) { return f == MARIN_KV_F32 ? 4 : 2; }
 
 constexpr int ROWS = 8;         // query rows per workgroup
 constexpr int MAX_CHUNK = 256;  // positions per workgroup
-constexpr int MIN_CHUNK = 64;
-constexpr int UNR = 8;  // position steps whose rows are loaded before any is used
+constexpr int MIN_CHUNK = 32;
+constexpr int MAX_SPLITS = 256;  // chunks of one context: two merge levels of at most 16
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
 
-// Eight values of a row starting at element d (d + 8 <= head_dim when VEC).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) const uint32_t g_u32;
+typedef __attribute__((address_space(1))) const uint16_t g_u16;
+
+// Eight values of a key or value row as stored (f32: two 16-byte words, f16/bf16: one). Page addresses are plain
+// integers; the loads go through global-address-space pointers so they are counted as vector-memory loads only.
+template <int F>
+struct Raw8 {
+    u32x4 w[F == MARIN_KV_F32 ? 2 : 1];
+};
+
+// Values d .. d + 7 of a row (VEC: d + 8 <= head_dim and 16-byte aligned; else element by element, zero past hd).
 template <int F, bool VEC>
-__device__ __forceinline__ void load8(const uint8_t *row, int d, int hd, float v[8]) {
+__device__ __forceinline__ void load_raw(const uint8_t *row, int d, int hd, Raw8<F> &r) {
+    constexpr int ES = F == MARIN_KV_F32 ? 4 : 2;
+    const uintptr_t base = (uintptr_t)row + (uintptr_t)d * ES;
     if constexpr (VEC) {
-        if constexpr (F == MARIN_KV_F32) {
-            const float4 a = *reinterpret_cast<const float4 *>(row + (size_t)d * 4);
-            const float4 b = *reinterpret_cast<const float4 *>(row + (size_t)d * 4 + 16);
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {
-            const uint4 u = *reinterpret_cast<const uint4 *>(row + (size_t)d * 2);
-            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (F == MARIN_KV_F16) {
-                    v[2 * i] = f16_bits_to_f32((uint16_t)(w[i] & 0xffffu));
-                    v[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16));
-                } else {
-                    v[2 * i] = __uint_as_float(w[i] << 16);
-                    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-                }
-            }
-        }
+        r.w[0] = *(g_u32x4 *)base;
+        if constexpr (F == MARIN_KV_F32) r.w[1] = *(g_u32x4 *)(base + 16);
     } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int e = d + i;
-            float x = 0.0f;
-            if (e < hd) {
-                if constexpr (F == MARIN_KV_F32) x = reinterpret_cast<const float *>(row)[e];
-                else if constexpr (F == MARIN_KV_F16) x = f16_bits_to_f32(reinterpret_cast<const uint16_t *>(row)[e]);
-                else x = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(row)[e]);
+            uint32_t x = 0;
+            if (d + i < hd) x = F == MARIN_KV_F32 ? *(g_u32 *)(base + 4 * i) : (uint32_t) * (g_u16 *)(base + 2 * i);
+            if constexpr (F == MARIN_KV_F32) {
+                r.w[i / 4][i % 4] = x;
+            } else {
+                if (i % 2 == 0) r.w[0][i / 2] = x;
+                else r.w[0][i / 2] |= x << 16;
             }
-            v[i] = x;
         }
     }
+}
+
+// Sum over aligned groups of N lanes (N = 1, 2, 4, 8, 16 or 32), every lane of a group getting the group's sum:
+// DPP quad permutes (xor 1, xor 2), half-row and row mirrors (8 and 16 lanes), then one cross-row swap for 32.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    auto dpp = [](float x, int ctrl_tag) {
+        int r = 0;
+        const int xi = __float_as_int(x);
+        switch (ctrl_tag) {
+            case 0: r = __builtin_amdgcn_update_dpp(0, xi, 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
+            case 1: r = __builtin_amdgcn_update_dpp(0, xi, 0x4E, 0xF, 0xF, false); break;   // quad_perm [2,3,0,1]
+            case 2: r = __builtin_amdgcn_update_dpp(0, xi, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+            default: r = __builtin_amdgcn_update_dpp(0, xi, 0x140, 0xF, 0xF, false); break; // row_mirror
+        }
+        return __int_as_float(r);
+    };
+    if constexpr (N >= 2) v += dpp(v, 0);
+    if constexpr (N >= 4) v += dpp(v, 1);
+    if constexpr (N >= 8) v += dpp(v, 2);
+    if constexpr (N >= 16) v += dpp(v, 3);
+    if constexpr (N >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+template <int F>
+__device__ __forceinline__ float elem(const Raw8<F> &r, int i) {
+    if constexpr (F == MARIN_KV_F32) return __uint_as_float(r.w[i / 4][i % 4]);
+    const uint32_t w = r.w[0][i / 2];
+    if constexpr (F == MARIN_KV_F16) return f16_bits_to_f32((uint16_t)(i % 2 ? w >> 16 : w & 0xffffu));
+    return __uint_as_float(i % 2 ? w & 0xffff0000u : w << 16);
 }
 
 __device__ __forceinline__ const uint8_t *kv_row(const uint64_t *table, const KvGeom &g, int which, int kvh,
@@ -71,14 +101,106 @@ __device__ __forceinline__ const uint8_t *kv_row(const uint64_t *table, const Kv
                                              (uint64_t)kvh * g.head_bytes + (uint64_t)in_page * g.head_dim * es);
 }
 
-// grid: x = chunk (split), y = kv_head * row_groups + row_group, z = sequence. LPP lanes per position, R query rows
-// (the heads of one kv head times the new tokens, in groups of R). The chunk's page addresses are read into LDS
-// first, so every row address is computed without another memory round trip.
-template <int F, int LPP, bool VEC, bool QBF16, int R>
-__global__ __launch_bounds__(256) void attention_partial(const void *__restrict__ qv, const uint64_t *__restrict__ tables,
-                                                         size_t table_stride, const uint32_t *__restrict__ ctx_lens,
-                                                         KvGeom geom, int tokens, int heads, int kv_heads, int chunk,
-                                                         int splits, float scale, float *__restrict__ part) {
+// Stores one value of a key/value row in the cache's format (kv_format.cu:48-72): f16 rounds to nearest and saturates
+// at the largest finite value (NaN stays NaN), bf16 rounds to nearest even (NaN stays NaN).
+template <int F>
+__device__ __forceinline__ void store_kv(uint8_t *row, int e, float x) {
+    if constexpr (F == MARIN_KV_F32) reinterpret_cast<float *>(row)[e] = x;
+    if constexpr (F == MARIN_KV_F16) {
+        const float c = fminf(fmaxf(x, -65504.0f), 65504.0f);
+        reinterpret_cast<_Float16 *>(row)[e] = (_Float16)(x != x ? x : c);
+    }
+    if constexpr (F == MARIN_KV_BF16) {
+        const unsigned u = __float_as_uint(x);
+        reinterpret_cast<uint16_t *>(row)[e] =
+            (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : (u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+}
+
+// RMSNorm(weight) then RoPE at `pos` of one head, by one wave: lane i takes the pairs (i, i + hd/2), i < hd/2 (hd even,
+// at most 256). Norm: x * (1 / sqrtf(mean(x^2) + eps)) * w (kernels.cu:51-60); RoPE: angle = pos * freq[i] with the
+// host's powf table, sincosf on the device, (a, b) -> (a cos - b sin, b cos + a sin) (ops.rs:56-95).
+__device__ __forceinline__ void norm_rope_head(const float *__restrict__ src, const float *__restrict__ w,
+                                               const float *__restrict__ freq, uint32_t pos, int hd, float eps,
+                                               int lane, float a[2], float b[2]) {
+    const int half = hd / 2;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = lane + 64 * k;
+        a[k] = i < half ? src[i] : 0.0f;
+        b[k] = i < half ? src[i + half] : 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) s += a[k] * a[k] + b[k] * b[k];
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const float scale = 1.0f / sqrtf(s / (float)hd + eps);
+    const float position = (float)pos;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = lane + 64 * k;
+        if (i >= half) continue;
+        const float x = a[k] * scale * w[i], y = b[k] * scale * w[i + half];
+        float sn, cs;
+        sincosf(position * freq[i], &sn, &cs);
+        a[k] = x * cs - y * sn;
+        b[k] = y * cs + x * sn;
+    }
+}
+
+#ifdef ATTN_TIMING
+__device__ unsigned long long attn_dbg[65536 * 8];
+#define ATT_T(k)                                                                                                 \
+    if (threadIdx.x == 0)                                                                                        \
+        attn_dbg[((size_t)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8 + (k)] = wall_clock64();
+extern "C" void marin_attn_dbg(void *out) { (void)hipMemcpyFromSymbol(out, HIP_SYMBOL(attn_dbg), sizeof(attn_dbg)); }
+extern "C" void marin_attn_dbg_clear() {
+    static unsigned long long zeros[65536 * 8];
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(attn_dbg), zeros, sizeof(zeros));
+}
+#else
+#define ATT_T(k)
+#endif
+
+// One launch of split-context attention. grid: x = chunk of the context (split), y = kv_head * row_groups + row_group,
+// z = sequence. A workgroup of NW waves takes `chunk` positions of one kv head for up to R query rows (row r of the kv
+// head: token r / group, head kvh * group + r % group). Lanes work in groups of LPP per position, 8 head values a
+// lane; each lane group loads the key and value rows of U positions together, so a chunk is one pass over HBM with an
+// online softmax per row. The chunk's page addresses are read into LDS first. Scores are kept in the log2 domain (the
+// host folds log2(e) into `scale`), so every weight is one hardware exp2.
+//
+// The chunks of a (sequence, kv head, row group) meet in the same launch, in two levels: each chunk writes a record
+// (max, sum of weights, weighted values) per row; the last chunk of every GROUP consecutive chunks to finish (an
+// atomic count, reset by that workgroup) merges the group's records with log-sum-exp weights, and the last group to
+// finish merges the group records into the output. Every sum runs in a fixed order, so results do not depend on
+// which workgroup finishes last. A context of one chunk writes the output directly.
+//
+// FUSE: q and the new tokens' keys and values are the raw projections [tokens][heads + 2 kv_heads][hd]; the kernel
+// applies q/k RMSNorm and RoPE itself and stores the new keys and values of its chunk into the cache before reading
+// it (every row group of the chunk stores the same bytes).
+constexpr int POS_IN_FLIGHT = 2;  // positions per lane group loaded together
+constexpr int GROUP = 16;         // chunks merged together at the first level
+
+// Records: [max, sum, 0, 0, values, pad] of rec_floats(hd) floats (a multiple of 4), written and read with 16-byte
+// agent-coherent buffer accesses (sc1): no dirty lines stay in one die's L2, so a merging workgroup on another die
+// reads them without a cache write-back. Level-1 records [unit][splits], then level-2 records [unit][groups].
+__host__ __device__ inline int rec_floats(int hd) { return (hd + 4 + 3) / 4 * 4; }
+__host__ __device__ inline int groups_of(int splits) { return (splits + GROUP - 1) / GROUP; }
+
+template <int R, int NW>
+struct MergeLds {
+    float mw[R][GROUP];  // record maxima, then weights
+    float lw[R][GROUP];
+};
+
+template <int F, int LPP, bool VEC, bool BF16IO, int R, bool FUSE, int NW>
+__global__ __launch_bounds__(64 * NW) void attention_split(
+    const void *__restrict__ qv, AttnFuse fuse, const uint64_t *__restrict__ tables, size_t table_stride,
+    const uint32_t *__restrict__ ctx_lens, KvGeom geom, int tokens, int heads, int kv_heads, int chunk, int splits,
+    float scale, float *__restrict__ part, int part_bytes, uint32_t *__restrict__ counters, void *__restrict__ out) {
+    constexpr int NT = 64 * NW;
+    constexpr int HMAX = 256;
+    constexpr int U = POS_IN_FLIGHT;
     constexpr int PPW = 64 / LPP;  // positions per wave step
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int slot = lane / LPP, sub = lane % LPP;
@@ -91,7 +213,9 @@ __global__ __launch_bounds__(256) void attention_partial(const void *__restrict_
     const int ctx = (int)ctx_lens[b];
     const int first = split * chunk;
     if (first >= ctx) return;
+    ATT_T(0);
     const int count = min(chunk, ctx - first);
+    const int used = (ctx + chunk - 1) / chunk;
     const int r0 = rg * R;
     const int nrows = min(R, total_rows - r0);
     const uint64_t *table = tables + (size_t)b * table_stride;
@@ -100,275 +224,425 @@ __global__ __launch_bounds__(256) void attention_partial(const void *__restrict_
     const uint64_t head_off = (uint64_t)kvh * geom.head_bytes + geom.layer_offset;
     const uint32_t pmask = (1u << geom.page_shift) - 1u;
 
-    __shared__ float w_s[R][MAX_CHUNK];
-    __shared__ float red[4][R][8 * 32];  // wave partial accumulators (only head_dim used)
-    __shared__ float ml_s[R][2];
     __shared__ uint64_t pages_s[MAX_CHUNK + 1];
+    __shared__ float q_s[R][HMAX];          // q rows; then the workgroup's (or a merge's) weighted values
+    __shared__ float red_acc[NW][R][HMAX];  // every wave's weighted values
+    __shared__ float red_ml[NW][R][2];      // every wave's maximum and sum
+    __shared__ float ml_s[R][2];            // the workgroup's (or a merge's) maximum and sum
+    __shared__ MergeLds<R, NW> mg;
+    __shared__ int last_s;
 
     const int page0 = first >> geom.page_shift;
     const int npages = ((first + count - 1) >> geom.page_shift) - page0 + 1;
-    for (int i = threadIdx.x; i < npages; i += 256) pages_s[i] = table[page0 + i] + head_off;
+    for (int i = threadIdx.x; i < npages; i += NT) pages_s[i] = table[page0 + i] + head_off;
 
-    // Query rows: row r = (token r / group, head kvh * group + r % group).
+    const size_t qkv_stride = (size_t)(heads + 2 * kv_heads) * hd;
+    if constexpr (FUSE) {
+        for (int r = wave; r < nrows; r += NW) {
+            const int rr = r0 + r, t = rr / group, h = kvh * group + rr % group;
+            float a2[2], b2[2];
+            norm_rope_head(fuse.qkv + (size_t)t * qkv_stride + (size_t)h * hd, fuse.q_norm, fuse.freq,
+                           (uint32_t)(ctx - tokens + t), hd, fuse.eps, lane, a2, b2);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int i = lane + 64 * k;
+                if (i < hd / 2) {
+                    q_s[r][i] = a2[k];
+                    q_s[r][i + hd / 2] = b2[k];
+                }
+            }
+        }
+        // the new positions that fall in this chunk: keys normalized and rotated, values as they are
+        for (int t = wave; t < tokens; t += NW) {
+            const int np = ctx - tokens + t;
+            if (np < first || np >= first + count) continue;
+            const uint64_t page = table[np >> geom.page_shift] + head_off + (uint64_t)(np & pmask) * hd * es;
+            uint8_t *krow = reinterpret_cast<uint8_t *>(page);
+            uint8_t *vrow = reinterpret_cast<uint8_t *>(page + geom.value_offset);
+            float a2[2], b2[2];
+            norm_rope_head(fuse.qkv + (size_t)t * qkv_stride + (size_t)(heads + kvh) * hd, fuse.k_norm, fuse.freq,
+                           (uint32_t)np, hd, fuse.eps, lane, a2, b2);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int i = lane + 64 * k;
+                if (i < hd / 2) {
+                    store_kv<F>(krow, i, a2[k]);
+                    store_kv<F>(krow, i + hd / 2, b2[k]);
+                }
+            }
+            const float *vsrc = fuse.qkv + (size_t)t * qkv_stride + (size_t)(heads + kv_heads + kvh) * hd;
+            for (int i = lane; i < hd; i += 64) store_kv<F>(vrow, i, vsrc[i]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < nrows * hd; i += NT) {
+            const int r = i / hd, e = i % hd;
+            const int rr = r0 + r, t = rr / group, h = kvh * group + rr % group;
+            const size_t at = (((size_t)b * tokens + t) * heads + h) * hd + e;
+            if constexpr (BF16IO) q_s[r][e] = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(qv)[at]);
+            else q_s[r][e] = reinterpret_cast<const float *>(qv)[at];
+        }
+    }
+    __syncthreads();
+    ATT_T(1);
+
     float q[R][8];
     int visible[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int rr = r0 + r;
-        const int t = rr / group, h = kvh * group + rr % group;
-        visible[r] = ctx - tokens + t + 1;
+        const int rr = r0 + r, t = rr / group;
+        visible[r] = r < nrows ? ctx - tokens + t + 1 : 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[r][i] = 0.0f;
-        if (r < nrows && d < hd) {
-            const size_t base = (((size_t)b * tokens + t) * heads + h) * hd;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (d + i < hd) {
-                    if constexpr (QBF16) q[r][i] = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(qv)[base + d + i]);
-                    else q[r][i] = reinterpret_cast<const float *>(qv)[base + d + i];
-                }
-            }
-        }
+        for (int i = 0; i < 8; ++i) q[r][i] = (d + i < hd) ? q_s[r][d + i] : 0.0f;
     }
-    __syncthreads();
     auto row_ptr = [&](int which, int p) {
         const uint32_t pos = (uint32_t)(first + p);
         return reinterpret_cast<const uint8_t *>(pages_s[(pos >> geom.page_shift) - page0] +
                                                  (which ? geom.value_offset : 0) + (uint64_t)(pos & pmask) * hd * es);
     };
 
-    // Scores: UNR rows per lane group are loaded before the dots, so each wave keeps UNR * 16 bytes per lane in flight.
-    for (int p0 = wave * PPW; p0 < count; p0 += 4 * PPW * UNR) {
-        float k[UNR][8];
+    float mrow[R], lrow[R], acc[R][8];
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int p = p0 + u * 4 * PPW + slot;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) k[u][i] = 0.0f;
-            if (p < count && d < hd) load8<F, VEC>(row_ptr(0, p), d, hd, k[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int p = p0 + u * 4 * PPW + slot;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float sc = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) sc += q[r][i] * k[u][i];
-#pragma unroll
-                for (int o = 1; o < LPP; o <<= 1) sc += __shfl_xor(sc, o);
-                if (sub == 0 && p < count && r < nrows)
-                    w_s[r][p] = (first + p < visible[r]) ? sc * scale : -INFINITY;
-            }
-        }
-    }
-    __syncthreads();
-
-    // Softmax pieces per row: the chunk maximum, exp(score - max), their sum.
-    for (int r = wave; r < nrows; r += 4) {
-        float m = -INFINITY;
-        for (int i = lane; i < count; i += 64) m = fmaxf(m, w_s[r][i]);
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        float l = 0.0f;
-        for (int i = lane; i < count; i += 64) {
-            const float e = m == -INFINITY ? 0.0f : expf(w_s[r][i] - m);
-            w_s[r][i] = e;
-            l += e;
-        }
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-        if (lane == 0) {
-            ml_s[r][0] = m;
-            ml_s[r][1] = l;
-        }
-    }
-    __syncthreads();
-
-    // Weighted values.
-    float acc[R][8];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r) {
+        mrow[r] = -INFINITY;
+        lrow[r] = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[r][i] = 0.0f;
-    for (int p0 = wave * PPW; p0 < count; p0 += 4 * PPW * UNR) {
-        float v[UNR][8];
+    }
+    constexpr int STEP = NW * PPW;
+    for (int p0 = wave * PPW; p0 < count; p0 += STEP * U) {
+        Raw8<F> kr[U], vr[U];
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int p = p0 + u * 4 * PPW + slot;
+        for (int u = 0; u < U; ++u) {
+            const int p = p0 + u * STEP + slot;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[u][i] = 0.0f;
-            if (p < count && d < hd) load8<F, VEC>(row_ptr(1, p), d, hd, v[u]);
+            for (int j = 0; j < (F == MARIN_KV_F32 ? 2 : 1); ++j) kr[u].w[j] = vr[u].w[j] = (u32x4){0, 0, 0, 0};
+            if (p < count && d < hd) {
+                load_raw<F, VEC>(row_ptr(0, p), d, hd, kr[u]);
+                load_raw<F, VEC>(row_ptr(1, p), d, hd, vr[u]);
+            }
         }
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int p = p0 + u * 4 * PPW + slot;
-            if (p < count) {
+        for (int r = 0; r < R; ++r) {
+            float sc[U];
+            float mx = -INFINITY;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float wgt = w_s[r][p];
+            for (int u = 0; u < U; ++u) {
+                float dot = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[r][i] += wgt * v[u][i];
+                for (int i = 0; i < 8; ++i) dot += q[r][i] * elem<F>(kr[u], i);
+                dot = group_sum<LPP>(dot);
+                const int p = p0 + u * STEP + slot;
+                sc[u] = (p < count && first + p < visible[r]) ? dot * scale : -INFINITY;
+                mx = fmaxf(mx, sc[u]);
+            }
+            const float mn = fmaxf(mrow[r], mx);
+            if (mn != -INFINITY) {
+                const float corr = __builtin_amdgcn_exp2f(mrow[r] - mn);
+                lrow[r] *= corr;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[r][i] *= corr;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const float e = __builtin_amdgcn_exp2f(sc[u] - mn);
+                    lrow[r] += e;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[r][i] += e * elem<F>(vr[u], i);
                 }
+                mrow[r] = mn;
             }
         }
     }
-    // Reduce over the position slots of the wave (lanes with the same sub), then over the waves.
+    // Combine the position slots of the wave (lanes with the same sub), then the waves in a fixed order.
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int o = LPP; o < 64; o <<= 1) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int r = 0; r < R; ++r) {
+            const float mo = __shfl_xor(mrow[r], o), lo = __shfl_xor(lrow[r], o);
+            float ao[8];
 #pragma unroll
-            for (int o = LPP; o < 64; o <<= 1) acc[r][i] += __shfl_xor(acc[r][i], o);
-    if (slot == 0 && d < hd) {
+            for (int i = 0; i < 8; ++i) ao[i] = __shfl_xor(acc[r][i], o);
+            const float mn = fmaxf(mrow[r], mo);
+            const float wa = mrow[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow[r] - mn);
+            const float wb = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
+            lrow[r] = lrow[r] * wa + lo * wb;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+            for (int i = 0; i < 8; ++i) acc[r][i] = acc[r][i] * wa + ao[i] * wb;
+            mrow[r] = mn;
+        }
+    }
+    if (slot == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (d + i < 8 * 32) red[wave][r][d + i] = acc[r][i];
-    }
-    __syncthreads();
-    for (int o = threadIdx.x; o < nrows * hd; o += 256) {
-        const int r = o / hd, e = o % hd;
-        const float v = (red[0][r][e] + red[1][r][e]) + (red[2][r][e] + red[3][r][e]);
-        const int rr = r0 + r;
-        const int t = rr / group, h = kvh * group + rr % group;
-        const size_t unit = (((size_t)b * tokens + t) * heads + h) * splits + split;
-        part[unit * (hd + 2) + 2 + e] = v;
-        if (e == 0) {
-            part[unit * (hd + 2)] = ml_s[r][0];
-            part[unit * (hd + 2) + 1] = ml_s[r][1];
+                if (d + i < hd) red_acc[wave][r][d + i] = acc[r][i];
+            if (sub == 0) {
+                red_ml[wave][r][0] = mrow[r];
+                red_ml[wave][r][1] = lrow[r];
+            }
         }
     }
-}
-
-// Combines the chunks of one (sequence, token, head): out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}. The
-// chunks' weights e^{m_s - M} are computed once into LDS, then each thread sums one element over the chunks.
-template <int OUT>
-__global__ __launch_bounds__(256) void attention_merge(const float *__restrict__ part,
-                                                       const uint32_t *__restrict__ ctx_lens, int tokens, int heads,
-                                                       int hd, int chunk, int splits, void *__restrict__ out) {
-    extern __shared__ float ws[];  // [splits] weights, then the total
-    const int unit = blockIdx.x;  // (b * tokens + t) * heads + h
-    const int b = unit / (tokens * heads);
-    const int used = min(splits, (int)((ctx_lens[b] + chunk - 1) / chunk));
-    const float *p = part + (size_t)unit * splits * (hd + 2);
-    __shared__ float red[4];
-    float m = -INFINITY;
-    for (int s = threadIdx.x; s < used; s += blockDim.x) m = fmaxf(m, p[(size_t)s * (hd + 2)]);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
-    m = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = fmaxf(m, red[w]);
-    for (int s = threadIdx.x; s < used; s += blockDim.x) {
-        const float ms = p[(size_t)s * (hd + 2)];
-        ws[s] = ms == -INFINITY ? 0.0f : expf(ms - m);
+    if (threadIdx.x < nrows) {
+        const int r = threadIdx.x;
+        float mn = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mn = fmaxf(mn, red_ml[w][r][0]);
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = red_ml[w][r][0];
+            l += mw == -INFINITY ? 0.0f : red_ml[w][r][1] * __builtin_amdgcn_exp2f(mw - mn);
+        }
+        ml_s[r][0] = mn;
+        ml_s[r][1] = l;
+    }
+    for (int o = threadIdx.x; o < nrows * hd; o += NT) {
+        const int r = o / hd, e = o % hd;
+        float mn = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mn = fmaxf(mn, red_ml[w][r][0]);
+        float a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = red_ml[w][r][0];
+            a += mw == -INFINITY ? 0.0f : red_acc[w][r][e] * __builtin_amdgcn_exp2f(mw - mn);
+        }
+        q_s[r][e] = a;
     }
     __syncthreads();
-    float total = 0.0f;
-    for (int s = 0; s < used; ++s) total += p[(size_t)s * (hd + 2) + 1] * ws[s];
-    for (int e = threadIdx.x; e < hd; e += blockDim.x) {
-        float acc = 0.0f;
-        for (int s = 0; s < used; ++s) acc += p[(size_t)s * (hd + 2) + 2 + e] * ws[s];
-        const float v = acc / total;
-        const size_t at = (size_t)unit * hd + e;
-        if constexpr (OUT == 0) reinterpret_cast<float *>(out)[at] = v;
-        if constexpr (OUT == 1) {
+    ATT_T(2);
+
+    auto write_out = [&](int r, int e, float v) {
+        const int rr = r0 + r, t = rr / group, h = kvh * group + rr % group;
+        const size_t at = (((size_t)b * tokens + t) * heads + h) * hd + e;
+        if constexpr (BF16IO) {
             const unsigned u = __float_as_uint(v);
             reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        } else {
+            reinterpret_cast<float *>(out)[at] = v;
         }
+    };
+    if (used == 1) {
+        for (int o = threadIdx.x; o < nrows * hd; o += NT) write_out(o / hd, o % hd, q_s[o / hd][o % hd] / ml_s[o / hd][1]);
+        return;
     }
+
+    const int RS = rec_floats(hd);
+    const int ngroups = groups_of(used);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, part_bytes, 0x00020000);
+    constexpr int SC1 = 16;
+    const size_t l2_base = (size_t)gridDim.z * tokens * heads * splits;  // first level-2 record
+    auto unit_of = [&](int r) {
+        const int rr = r0 + r, t = rr / group, h = kvh * group + rr % group;
+        return ((size_t)b * tokens + t) * heads + h;
+    };
+    auto l1_off = [&](int r, int sp) { return (int)((unit_of(r) * splits + sp) * (size_t)RS * 4); };
+    auto l2_off = [&](int r, int gi) {
+        return (int)((l2_base + unit_of(r) * (size_t)groups_of(splits) + gi) * (size_t)RS * 4);
+    };
+    // Writes the workgroup's current (ml_s, q_s) as a record.
+    auto write_record = [&](auto off_of) {
+        for (int o = threadIdx.x; o < nrows * (RS / 4); o += NT) {
+            const int r = o / (RS / 4), c4 = o % (RS / 4);
+            u32x4 v;
+            if (c4 == 0) {
+                v = (u32x4){__float_as_uint(ml_s[r][0]), __float_as_uint(ml_s[r][1]), 0u, 0u};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * (c4 - 1) + j;
+                    v[j] = e < hd ? __float_as_uint(q_s[r][e]) : 0u;
+                }
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, prs, off_of(r) + 16 * c4, 0, SC1);
+        }
+        // every wave's stores acknowledged before the workgroup counts itself in
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+    // Counts the workgroup in; true for the last of `n`.
+    auto arrive = [&](uint32_t *counter, int n) {
+        if (threadIdx.x == 0)
+            last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(n - 1);
+        __syncthreads();
+        return last_s != 0;
+    };
+    // Merges n (<= GROUP) records at off_of(r, k) into (ml_s, q_s), sums in record order.
+    auto merge = [&](auto off_of, int n) {
+        for (int i = threadIdx.x; i < nrows * n; i += NT) {
+            const int r = i / n, k = i - r * n;
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prs, off_of(r, k), 0, SC1);
+            mg.mw[r][k] = __uint_as_float(v[0]);
+            mg.lw[r][k] = __uint_as_float(v[1]);
+        }
+        __syncthreads();
+        if (threadIdx.x < nrows) {
+            const int r = threadIdx.x;
+            float mn = -INFINITY;
+            for (int k = 0; k < n; ++k) mn = fmaxf(mn, mg.mw[r][k]);
+            float l = 0.0f;
+            for (int k = 0; k < n; ++k) {
+                const float mk = mg.mw[r][k];
+                const float wt = mk == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mk - mn);
+                mg.mw[r][k] = wt;
+                l += mg.lw[r][k] * wt;
+            }
+            ml_s[r][0] = mn;
+            ml_s[r][1] = l;
+        }
+        __syncthreads();
+        const int c4 = (hd + 3) / 4;
+        for (int col = threadIdx.x; col < nrows * c4; col += NT) {
+            const int r = col / c4, e4 = col - r * c4;
+            u32x4 v[GROUP];
+#pragma unroll
+            for (int k = 0; k < GROUP; ++k)
+                v[k] = __builtin_amdgcn_raw_buffer_load_b128(prs, off_of(r, min(k, n - 1)) + 16 * (1 + e4), 0, SC1);
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < GROUP; ++k) {
+                const float wt = k < n ? mg.mw[r][k] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] += __uint_as_float(v[k][j]) * wt;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * e4 + j < hd) q_s[r][4 * e4 + j] = a[j];
+        }
+        __syncthreads();
+    };
+
+    // level 1: this chunk's record; the last of its group merges the group
+    write_record([&](int r) { return l1_off(r, split); });
+    ATT_T(3);
+    const int gi = split / GROUP;
+    const int gsize = min(GROUP, used - gi * GROUP);
+    const size_t cbase = (((size_t)b * kv_heads + kvh) * row_groups + rg) * (size_t)(1 + groups_of(splits));
+    uint32_t *c1 = counters + cbase + 1 + gi;
+    if (!arrive(c1, gsize)) return;
+    ATT_T(4);
+    merge([&](int r, int k) { return l1_off(r, gi * GROUP + k); }, gsize);
+    if (threadIdx.x == 0) __hip_atomic_store(c1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ATT_T(5);
+    if (ngroups > 1) {
+        // level 2: the group's record; the last group merges the groups
+        write_record([&](int r) { return l2_off(r, gi); });
+        uint32_t *c2 = counters + cbase;
+        if (!arrive(c2, ngroups)) return;
+        ATT_T(6);
+        merge([&](int r, int k) { return l2_off(r, k); }, ngroups);
+        if (threadIdx.x == 0) __hip_atomic_store(c2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ATT_T(7);
+    for (int o = threadIdx.x; o < nrows * hd; o += NT) write_out(o / hd, o % hd, q_s[o / hd][o % hd] / ml_s[o / hd][1]);
 }
 
-// Positions per workgroup: enough workgroups for about two per compute unit, 64 to 256 positions each.
-static int chunk_for(size_t max_ctx, size_t blocks_per_chunk, int cu_count) {
-    const size_t wanted = std::max<size_t>(1, (2 * (size_t)std::max(cu_count, 1) + blocks_per_chunk - 1) /
-                                                  std::max<size_t>(blocks_per_chunk, 1));
+#ifndef ATTN_NW
+#define ATTN_NW 4
+#endif
+#ifndef ATTN_BPC
+#define ATTN_BPC 4
+#endif
+constexpr int NWAVES = ATTN_NW;          // waves per attention workgroup
+constexpr int BLOCKS_PER_CU = ATTN_BPC;  // workgroups the chunk size aims at per compute unit
+
+// Positions per workgroup: about BLOCKS_PER_CU workgroups per compute unit, MIN_CHUNK to MAX_CHUNK positions each,
+// rounded up to what one step of the workgroup's lanes covers so no lane group idles.
+static int chunk_for(size_t max_ctx, size_t blocks_per_chunk, int cu_count, size_t granule) {
+    const size_t target = (size_t)BLOCKS_PER_CU * (size_t)std::max(cu_count, 1);
+    const size_t wanted = std::max<size_t>(1, (target + blocks_per_chunk - 1) / std::max<size_t>(blocks_per_chunk, 1));
     size_t chunk = (max_ctx + wanted - 1) / wanted;
+    granule = std::min<size_t>(granule, MAX_CHUNK);
+    chunk = (chunk + granule - 1) / granule * granule;
     chunk = std::min<size_t>(MAX_CHUNK, std::max<size_t>(MIN_CHUNK, chunk));
     return (int)chunk;
 }
 
+static size_t record_count(size_t units, size_t splits) { return units * (splits + groups_of((int)splits)); }
+
 size_t attention_partial_floats(size_t batch, size_t tokens, size_t heads, size_t head_dim, size_t max_ctx,
                                 int cu_count) {
     (void)cu_count;
-    const size_t splits = (max_ctx + MIN_CHUNK - 1) / MIN_CHUNK;
-    return batch * tokens * heads * std::max<size_t>(splits, 1) * (head_dim + 2);
+    const size_t splits = std::max<size_t>(std::min<size_t>((max_ctx + MIN_CHUNK - 1) / MIN_CHUNK, MAX_SPLITS), 1);
+    return record_count(batch * tokens * heads, splits) * (size_t)rec_floats((int)head_dim);
 }
 
-template <int F, int LPP, bool VEC, int R>
-static void launch_partial_r(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
-    if (a.q_bf16)
-        attention_partial<F, LPP, VEC, true, R><<<grid, dim3(256), 0, g->stream>>>(
-            a.q, a.tables, a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk, splits,
-            scale, a.partials);
-    else
-        attention_partial<F, LPP, VEC, false, R><<<grid, dim3(256), 0, g->stream>>>(
-            a.q, a.tables, a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk, splits,
-            scale, a.partials);
+size_t attention_counters(size_t batch, size_t tokens, size_t heads) {
+    return std::max<size_t>(batch * tokens * heads, 1) * (1 + MAX_SPLITS / GROUP);
 }
 
 static int rows_per_block(const AttentionArgs &a) {
-    const size_t rows = a.tokens * (a.heads / a.kv_heads);
-    return rows <= 2 ? 2 : (rows <= 4 ? 4 : ROWS);
+    return a.tokens * (a.heads / a.kv_heads) <= 4 ? 4 : ROWS;
+}
+
+template <int F, int LPP, bool VEC, bool BF16IO, int R, bool FUSE>
+static void launch_split(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    attention_split<F, LPP, VEC, BF16IO, R, FUSE, NWAVES><<<grid, dim3(64 * NWAVES), 0, g->stream>>>(
+        a.q, a.fuse, a.tables, a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk,
+        splits, scale, a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+}
+
+template <int F, int LPP, bool VEC, int R>
+static void launch_split_r(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    if (a.fuse.qkv) launch_split<F, LPP, VEC, false, R, true>(g, a, grid, chunk, splits, scale);
+    else if (a.bf16_io) launch_split<F, LPP, VEC, true, R, false>(g, a, grid, chunk, splits, scale);
+    else launch_split<F, LPP, VEC, false, R, false>(g, a, grid, chunk, splits, scale);
 }
 
 template <int F, int LPP, bool VEC>
-static void launch_partial(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
-    const int r = rows_per_block(a);
-    if (r == 2) launch_partial_r<F, LPP, VEC, 2>(g, a, grid, chunk, splits, scale);
-    else if (r == 4) launch_partial_r<F, LPP, VEC, 4>(g, a, grid, chunk, splits, scale);
-    else launch_partial_r<F, LPP, VEC, ROWS>(g, a, grid, chunk, splits, scale);
+static void launch_split_l(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    if (rows_per_block(a) == 4) launch_split_r<F, LPP, VEC, 4>(g, a, grid, chunk, splits, scale);
+    else launch_split_r<F, LPP, VEC, ROWS>(g, a, grid, chunk, splits, scale);
+}
+
+// Lanes per position, 8 head values a lane (at least 4 lanes); head sizes that are not a multiple of 8 take the
+// element-wise loads with 32 lanes.
+static int lanes_for(size_t hd) {
+    if (hd % 8) return 32;
+    int lanes = 4;
+    while ((size_t)lanes * 8 < hd) lanes <<= 1;
+    return lanes;
 }
 
 template <int F>
-static void launch_partial_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
-    const int hd = (int)a.geom.head_dim;
-    const bool vec = hd % 8 == 0;
-    int lpp = 1;
-    while (lpp * 8 < hd) lpp <<= 1;
-#define MARIN_P(L)                                                                    \
-    do {                                                                              \
-        if (vec) launch_partial<F, L, true>(g, a, grid, chunk, splits, scale);        \
-        else launch_partial<F, L, false>(g, a, grid, chunk, splits, scale);           \
-    } while (0)
-    switch (lpp) {
-        case 1: MARIN_P(1); break;
-        case 2: MARIN_P(2); break;
-        case 4: MARIN_P(4); break;
-        case 8: MARIN_P(8); break;
-        case 16: MARIN_P(16); break;
-        default: MARIN_P(32); break;
+static void launch_split_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    const size_t hd = a.geom.head_dim;
+    switch (lanes_for(hd)) {
+        case 4: launch_split_l<F, 4, true>(g, a, grid, chunk, splits, scale); break;
+        case 8: launch_split_l<F, 8, true>(g, a, grid, chunk, splits, scale); break;
+        case 16: launch_split_l<F, 16, true>(g, a, grid, chunk, splits, scale); break;
+        default:
+            if (hd % 8) launch_split_l<F, 32, false>(g, a, grid, chunk, splits, scale);
+            else launch_split_l<F, 32, true>(g, a, grid, chunk, splits, scale);
     }
-#undef MARIN_P
 }
 
 void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     const size_t group = a.heads / a.kv_heads;
     const size_t rpb = (size_t)rows_per_block(a);
     const size_t row_groups = (a.tokens * group + rpb - 1) / rpb;
-    const int chunk = chunk_for(a.max_ctx, a.kv_heads * row_groups * a.batch, g->cu_count);
+    if (a.geom.head_dim == 0 || a.geom.head_dim > 256) unsupported("head size", 256, a.geom.head_dim);
+    if (a.fuse.qkv && a.geom.head_dim % 2) unsupported("head size for RoPE (even)", 256, a.geom.head_dim);
+    const size_t per_step = (size_t)NWAVES * (64 / lanes_for(a.geom.head_dim)) * POS_IN_FLIGHT;
+    const int chunk = chunk_for(a.max_ctx, a.kv_heads * row_groups * a.batch, g->cu_count, per_step);
     const int splits = (int)((a.max_ctx + chunk - 1) / chunk);
-    if ((size_t)splits * a.batch * a.tokens * a.heads * (a.geom.head_dim + 2) > a.partial_floats)
-        shape("attention partial sums", (size_t)splits * a.batch * a.tokens * a.heads * (a.geom.head_dim + 2),
-              a.partial_floats);
-    const float scale = 1.0f / sqrtf((float)a.geom.head_dim);
+    if (splits > MAX_SPLITS) unsupported("attention context (positions)", (size_t)MAX_SPLITS * MAX_CHUNK, a.max_ctx);
+    const size_t need = record_count(a.batch * a.tokens * a.heads, splits) * (size_t)rec_floats((int)a.geom.head_dim);
+    if (need > a.partial_floats) shape("attention partial records (floats)", need, a.partial_floats);
+    if (a.partial_floats * 4 >= ((size_t)1 << 31))
+        unsupported("attention partial bytes", (size_t)1 << 31, a.partial_floats * 4);
+    const size_t counters = a.batch * a.kv_heads * row_groups * (1 + groups_of(splits));
+    if (counters > a.counter_count) shape("attention chunk counters", counters, a.counter_count);
+    // scores in the log2 domain: dot * (1/sqrt(hd)) * log2(e), weights 2^(s - max) with the hardware exp2
+    const float scale = (float)(1.4426950408889634 / std::sqrt((double)a.geom.head_dim));
     dim3 grid((unsigned)splits, (unsigned)(a.kv_heads * row_groups), (unsigned)a.batch);
     switch (a.geom.format) {
-        case MARIN_KV_F32: launch_partial_f<MARIN_KV_F32>(g, a, grid, chunk, splits, scale); break;
-        case MARIN_KV_F16: launch_partial_f<MARIN_KV_F16>(g, a, grid, chunk, splits, scale); break;
-        default: launch_partial_f<MARIN_KV_BF16>(g, a, grid, chunk, splits, scale); break;
+        case MARIN_KV_F32: launch_split_f<MARIN_KV_F32>(g, a, grid, chunk, splits, scale); break;
+        case MARIN_KV_F16: launch_split_f<MARIN_KV_F16>(g, a, grid, chunk, splits, scale); break;
+        default: launch_split_f<MARIN_KV_BF16>(g, a, grid, chunk, splits, scale); break;
     }
     g->launched(marin_gpu::ATTENTION, a.bytes_hint);
-    const dim3 mgrid((unsigned)(a.batch * a.tokens * a.heads));
-    const dim3 mblock((unsigned)std::min<size_t>(256, (a.geom.head_dim + 63) / 64 * 64));
-    const size_t mlds = (size_t)splits * 4;
-    if (a.out_kind == 0)
-        attention_merge<0><<<mgrid, mblock, mlds, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
-                                                               (int)a.geom.head_dim, chunk, splits, a.out);
-    else
-        attention_merge<1><<<mgrid, mblock, mlds, g->stream>>>(a.partials, a.ctx, (int)a.tokens, (int)a.heads,
-                                                               (int)a.geom.head_dim, chunk, splits, a.out);
-    g->launched(marin_gpu::ATTENTION, 0.0);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -382,17 +656,7 @@ __global__ void kv_store_kernel(const float *__restrict__ keys, const float *__r
     for (int e = threadIdx.x; e < hd; e += blockDim.x) {
         for (int which = 0; which < 2; ++which) {
             const float x = (which ? values : keys)[((size_t)t * kv_heads + kvh) * hd + e];
-            uint8_t *row = const_cast<uint8_t *>(kv_row(pages, geom, which, kvh, start + t));
-            if constexpr (F == MARIN_KV_F32) reinterpret_cast<float *>(row)[e] = x;
-            if constexpr (F == MARIN_KV_F16) {
-                const float c = fminf(fmaxf(x, -65504.0f), 65504.0f);
-                reinterpret_cast<_Float16 *>(row)[e] = (_Float16)(x != x ? x : c);
-            }
-            if constexpr (F == MARIN_KV_BF16) {
-                const unsigned u = __float_as_uint(x);
-                reinterpret_cast<uint16_t *>(row)[e] =
-                    (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : (u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-            }
+            store_kv<F>(const_cast<uint8_t *>(kv_row(pages, geom, which, kvh, start + t)), e, x);
         }
     }
 }
@@ -474,7 +738,7 @@ size_t marin_kv_startup_bytes(size_t layers, size_t heads, size_t kv_heads, size
     if (__builtin_mul_overflow(row, (size_t)MARIN_PAGE_TOKENS * MARIN_SLAB_PAGES * 2, &slab)) return 0;
     if (__builtin_mul_overflow(slab, layers, &slab)) return 0;
     table = std::max<size_t>(1, (capacity + MARIN_PAGE_TOKENS - 1) / MARIN_PAGE_TOKENS) * 8;
-    scratch = attention_partial_floats(1, 8, heads, head_dim, capacity, 0) * 4;
+    scratch = attention_partial_floats(1, 8, heads, head_dim, capacity, 0) * 4 + attention_counters(1, 8, heads) * 4;
     return slab + table + scratch + 4;
 }
 
@@ -504,6 +768,7 @@ marin_status marin_kv_new(marin_gpu *g, size_t layers, size_t heads, size_t kv_h
             kv->ctx = (uint32_t *)g->alloc(4, true);
             kv->partial_floats = attention_partial_floats(1, 8, heads, head_dim, std::max<size_t>(capacity, 1), g->cu_count);
             kv->partials = (float *)g->alloc(kv->partial_floats * 4, false);
+            kv->counters = (uint32_t *)g->alloc(attention_counters(1, 8, heads) * 4, true);
         } catch (...) {
             marin_kv_free(kv);
             throw;
@@ -519,6 +784,7 @@ void marin_kv_free(marin_kv *kv) {
     kv->gpu->release(kv->page_ptrs);
     kv->gpu->release(kv->ctx);
     kv->gpu->release(kv->partials);
+    kv->gpu->release(kv->counters);
     delete kv;
 }
 
@@ -610,9 +876,8 @@ marin_status marin_attention(marin_gpu *g, const marin_buffer *q, marin_kv *kv, 
             HIP_CHECK(hipMemcpyAsync(kv->ctx, staged, 4, hipMemcpyHostToDevice, g->stream));
             AttentionArgs a{};
             a.q = (const float *)q->data + t0 * heads * hd;
-            a.q_bf16 = false;
+            a.bf16_io = false;
             a.out = (float *)out->data + t0 * heads * hd;
-            a.out_kind = 0;
             a.tables = kv->page_ptrs;
             a.table_stride = 0;
             a.ctx = kv->ctx;
@@ -624,6 +889,8 @@ marin_status marin_attention(marin_gpu *g, const marin_buffer *q, marin_kv *kv, 
             a.max_ctx = ctx;
             a.partials = kv->partials;
             a.partial_floats = kv->partial_floats;
+            a.counters = kv->counters;
+            a.counter_count = attention_counters(1, 8, heads);
             launch_attention(g, a);
         }
     });
@@ -644,6 +911,8 @@ struct marin_page_pool {
     size_t ctx_cap = 0;
     float *partials = nullptr;
     size_t partial_floats = 0;
+    uint32_t *counters = nullptr;
+    size_t counter_count = 0;
     std::vector<uint64_t> last_tables;  // what the device copies hold, to skip unchanged uploads
     std::vector<uint32_t> last_ctx;
 };
@@ -681,6 +950,7 @@ void marin_page_pool_free(marin_page_pool *p) {
     p->gpu->release(p->tables);
     p->gpu->release(p->ctx);
     p->gpu->release(p->partials);
+    p->gpu->release(p->counters);
     delete p;
 }
 
@@ -738,6 +1008,13 @@ marin_status marin_paged_attention_batch(marin_gpu *g, const marin_buffer *q, ma
             p->partials = (float *)g->alloc(need_partials * 4, false);
             p->partial_floats = need_partials;
         }
+        const size_t need_counters = attention_counters(batch, 1, heads);
+        if (need_counters > p->counter_count) {
+            g->release(p->counters);
+            p->counters = nullptr;
+            p->counters = (uint32_t *)g->alloc(need_counters * 4, true);
+            p->counter_count = need_counters;
+        }
         if (p->last_tables != addr) {
             g->upload(p->tables, addr.data(), addr.size() * 8);
             p->last_tables = addr;
@@ -749,9 +1026,8 @@ marin_status marin_paged_attention_batch(marin_gpu *g, const marin_buffer *q, ma
         }
         AttentionArgs a{};
         a.q = q->data;
-        a.q_bf16 = true;
+        a.bf16_io = true;
         a.out = out->data;
-        a.out_kind = 1;
         a.tables = p->tables;
         a.table_stride = table_stride;
         a.ctx = p->ctx;
@@ -768,6 +1044,8 @@ marin_status marin_paged_attention_batch(marin_gpu *g, const marin_buffer *q, ma
         a.max_ctx = max_ctx;
         a.partials = p->partials;
         a.partial_floats = p->partial_floats;
+        a.counters = p->counters;
+        a.counter_count = p->counter_count;
         launch_attention(g, a);
     });
 }

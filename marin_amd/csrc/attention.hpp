@@ -60,11 +60,19 @@ size_t kv_elem_bytes(marin_kv_format f);
 // Attention of `tokens` new tokens of `batch` sequences. q/out: [batch][tokens][heads][head_dim] in q_bf16/out_*
 // types. tables: device u64 page addresses [batch][table_stride]. ctx: device u32 [batch] (visible positions
 // including the new tokens). Partials must hold batch*tokens*heads*splits*(head_dim+2) floats.
+// Raw projections for the fused path: q and the new tokens' keys and values as [tokens][heads + 2 kv_heads][hd] f32,
+// with the q/k RMSNorm weights and the RoPE frequency table (batch 1).
+struct AttnFuse {
+    const float *qkv = nullptr;
+    const float *q_norm = nullptr, *k_norm = nullptr, *freq = nullptr;
+    float eps = 0.0f;
+};
+
 struct AttentionArgs {
-    const void *q;
-    bool q_bf16;
+    const void *q;   // [batch][tokens][heads][head_dim], f32 or bf16 (bf16_io); unused with fuse.qkv
+    bool bf16_io;    // q and out in bf16 instead of f32
     void *out;
-    int out_kind;  // 0 f32, 1 bf16
+    AttnFuse fuse;   // fuse.qkv set: q/k norm + RoPE + the store of the new keys/values happen in the kernel
     const uint64_t *tables;
     size_t table_stride;
     const uint32_t *ctx;  // device
@@ -73,10 +81,14 @@ struct AttentionArgs {
     size_t max_ctx;  // bound on every ctx[b], sets the grid
     float *partials;
     size_t partial_floats;
+    uint32_t *counters;  // zero-initialized; every launch leaves them zero
+    size_t counter_count;
     double bytes_hint = 0.0;  // algorithmic bytes, for launch accounting only
 };
 size_t attention_partial_floats(size_t batch, size_t tokens, size_t heads, size_t head_dim, size_t max_ctx,
                                 int cu_count);
+// Chunk counters a launch of `batch` sequences of `tokens` new tokens can use.
+size_t attention_counters(size_t batch, size_t tokens, size_t heads);
 void launch_attention(marin_gpu *g, const AttentionArgs &a);
 
 // Stores f32 keys/values [tokens][kv_heads*head_dim] at positions start.. of one layer.
@@ -97,6 +109,7 @@ struct marin_kv {
     uint32_t *ctx = nullptr;  // device scalar used by the kernels
     float *partials = nullptr;
     size_t partial_floats = 0;
+    uint32_t *counters = nullptr;
 
     size_t row_bytes() const { return kv_heads * head_dim * marin::kv_elem_bytes(format); }
     size_t page_bytes() const { return row_bytes() * MARIN_PAGE_TOKENS * layers * 2; }

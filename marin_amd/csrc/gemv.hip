@@ -153,10 +153,10 @@ __global__ __launch_bounds__(64 * GW) void gemv_q(const uint8_t *__restrict__ co
         const int gi = (u * UC) / group;
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
-            const uint8_t *rowp = codes + (size_t)((tile0 + r) * 16 + c) * row_bytes + CB * q;
+            const uint8_t *rowp = codes + (size_t)(tile0 + r) * 16 * row_bytes + CB * lane;
 #pragma unroll
             for (int w = 0; w < UW; ++w) {
-                const size_t off = (size_t)(u * UW + w) * (BITS == 8 ? 64 : 32);
+                const size_t off = (size_t)(u * UW + w) * 64 * CB;
                 if constexpr (BITS == 8)
                     dst[r][w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(rowp + off));
                 else
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(64 * GW) void gemv_q(const uint8_t *__restrict__ co
 }
 
 bool gemv_supported(const marin_quant_matrix *w) {
-    return (w->bits == 8 || w->bits == 4) && w->group % 64 == 0 && w->cols % 64 == 0;
+    return (w->bits == 8 || w->bits == 4) && w->windowed;
 }
 
 template <int BITS, int RT, int UW, typename ST>

@@ -28,101 +28,6 @@ namespace marin {
 
 constexpr size_t CHUNK = GEMV_TOKENS;  // tokens per pass through the layers
 
-// Per (token, head): q heads get RMSNorm(q_norm) + RoPE into q; k heads RMSNorm(k_norm) + RoPE into the cache; v heads
-// go to the cache as they are. grid (tokens, heads + 2 * kv_heads), 64 threads; thread i takes the pairs (i, i + hd/2).
-template <int F>
-__global__ __launch_bounds__(64) void qk_norm_rope_store(const float *__restrict__ qkv, float *__restrict__ q_out,
-                                                         const float *__restrict__ q_norm,
-                                                         const float *__restrict__ k_norm,
-                                                         const float *__restrict__ freq, const uint64_t *__restrict__ pages,
-                                                         KvGeom geom, const uint32_t *__restrict__ state, int heads,
-                                                         int kv_heads, float eps) {
-    const int t = blockIdx.x, j = blockIdx.y, lane = threadIdx.x;
-    const int hd = (int)geom.head_dim, half = hd / 2;
-    const int qd = heads * hd, kvd = kv_heads * hd;
-    const uint32_t pos = state[0] + t;
-    const float *src;
-    int kind, kvh = 0;
-    if (j < heads) {
-        kind = 0;
-        src = qkv + (size_t)t * (qd + 2 * kvd) + (size_t)j * hd;
-    } else if (j < heads + kv_heads) {
-        kind = 1;
-        kvh = j - heads;
-        src = qkv + (size_t)t * (qd + 2 * kvd) + qd + (size_t)kvh * hd;
-    } else {
-        kind = 2;
-        kvh = j - heads - kv_heads;
-        src = qkv + (size_t)t * (qd + 2 * kvd) + qd + kvd + (size_t)kvh * hd;
-    }
-    constexpr int MAXP = 2;  // head_dim <= 256
-    float a[MAXP], b[MAXP];
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k) {
-        const int i = lane + 64 * k;
-        a[k] = i < half ? src[i] : 0.0f;
-        b[k] = i < half ? src[i + half] : 0.0f;
-    }
-    if (kind != 2) {
-        float s = 0.0f;
-#pragma unroll
-        for (int k = 0; k < MAXP; ++k) s += a[k] * a[k] + b[k] * b[k];
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-        const float scale = 1.0f / sqrtf(s / (float)hd + eps);
-        const float *w = kind == 0 ? q_norm : k_norm;
-        const float position = (float)pos;
-#pragma unroll
-        for (int k = 0; k < MAXP; ++k) {
-            const int i = lane + 64 * k;
-            if (i >= half) continue;
-            const float x = a[k] * scale * w[i], y = b[k] * scale * w[i + half];
-            float sn, cs;
-            sincosf(position * freq[i], &sn, &cs);
-            a[k] = x * cs - y * sn;
-            b[k] = y * cs + x * sn;
-        }
-    }
-    if (kind == 0) {
-        float *dst = q_out + (size_t)t * qd + (size_t)j * hd;
-#pragma unroll
-        for (int k = 0; k < MAXP; ++k) {
-            const int i = lane + 64 * k;
-            if (i < half) {
-                dst[i] = a[k];
-                dst[i + half] = b[k];
-            }
-        }
-        return;
-    }
-    const uint64_t page = pages[pos >> geom.page_shift];
-    const uint32_t in_page = pos & ((1u << geom.page_shift) - 1u);
-    const size_t es = F == MARIN_KV_F32 ? 4 : 2;
-    uint8_t *row = reinterpret_cast<uint8_t *>(page + geom.layer_offset + (kind == 2 ? geom.value_offset : 0) +
-                                               (uint64_t)kvh * geom.head_bytes + (uint64_t)in_page * hd * es);
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k) {
-        const int i = lane + 64 * k;
-        if (i >= half) continue;
-        const float vals[2] = {a[k], b[k]};
-        const int idx[2] = {i, i + half};
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const float x = vals[u];
-            if constexpr (F == MARIN_KV_F32) reinterpret_cast<float *>(row)[idx[u]] = x;
-            if constexpr (F == MARIN_KV_F16) {
-                const float c = fminf(fmaxf(x, -65504.0f), 65504.0f);
-                reinterpret_cast<_Float16 *>(row)[idx[u]] = (_Float16)(x != x ? x : c);
-            }
-            if constexpr (F == MARIN_KV_BF16) {
-                const unsigned uu = __float_as_uint(x);
-                reinterpret_cast<uint16_t *>(row)[idx[u]] =
-                    (uint16_t)((uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
-                                                                : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
-            }
-        }
-    }
-}
-
 // One decode step's bookkeeping, after the output head left the greedy choice in *best as (total-order key, ~id)
 // (sampler/src/lib.rs:40-48: largest logit, lowest id on ties): record the token, clear the choice for the next
 // head, advance the state (pos += 1, ctx = pos + 1, step += 1) and embed the token's table row into hidden.
@@ -146,7 +51,7 @@ __global__ __launch_bounds__(512) void advance(unsigned long long *best, uint32_
     const int groups = cols / group;
     const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
     for (int i = threadIdx.x; i < cols; i += blockDim.x)
-        hidden[i] = (float)(int8_t)codes[row * cols + i] * srow[(i / group) * 16];
+        hidden[i] = (float)(int8_t)codes[code_offset(row, i, cols, true, 16)] * srow[(i / group) * 16];
 }
 
 // Sets the device state for a pass of `count` tokens at `pos` (pos, ctx = pos + count) and clears the greedy choice
@@ -163,7 +68,8 @@ __global__ void embed_device_ids(const uint8_t *__restrict__ codes, const float 
     const int groups = cols / group;
     const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
     for (int i = threadIdx.x; i < cols; i += blockDim.x)
-        out[(size_t)blockIdx.x * cols + i] = (float)(int8_t)codes[row * cols + i] * srow[(i / group) * 16];
+        out[(size_t)blockIdx.x * cols + i] =
+            (float)(int8_t)codes[code_offset(row, i, cols, true, 16)] * srow[(i / group) * 16];
 }
 
 }  // namespace marin
@@ -189,12 +95,13 @@ struct marin_qwen3_cache {
     marin_qwen3 *model = nullptr;
     marin_kv *kv = nullptr;
     // device workspace, CHUNK tokens
-    float *hidden = nullptr, *qkv = nullptr, *q = nullptr, *ctx = nullptr, *act = nullptr, *logits = nullptr;
+    float *hidden = nullptr, *qkv = nullptr, *ctx = nullptr, *act = nullptr, *logits = nullptr;
     uint32_t *ids = nullptr, *state = nullptr, *tokens_out = nullptr;
     unsigned long long *best = nullptr;  // greedy choice of the last pass (key, ~id)
     size_t tokens_cap = 0;
     float *attn_partials = nullptr;
     size_t attn_partial_floats = 0;
+    uint32_t *attn_counters = nullptr;
     hipGraphExec_t graph = nullptr;
     size_t graph_capacity_ctx = 0;
 };
@@ -309,21 +216,15 @@ static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx,
         qkv_out.y_stride = qd + 2 * kvd;
         launch_gemv(g, L.qkv, norm_in, qkv_out, n);
         const KvGeom geom = c->kv->geom(l);
-        dim3 grid((unsigned)n, (unsigned)(cfg.heads + 2 * cfg.kv_heads));
-#define MARIN_QK(F)                                                                                                 \
-    qk_norm_rope_store<F><<<grid, dim3(64), 0, g->stream>>>(c->qkv, c->q, L.q_norm, L.k_norm, m->freq,               \
-                                                          c->kv->page_ptrs, geom, c->state, (int)cfg.heads,          \
-                                                          (int)cfg.kv_heads, cfg.rms_eps)
-        if (c->kv->format == MARIN_KV_F32) MARIN_QK(MARIN_KV_F32);
-        else if (c->kv->format == MARIN_KV_F16) MARIN_QK(MARIN_KV_F16);
-        else MARIN_QK(MARIN_KV_BF16);
-#undef MARIN_QK
-        g->launched();
         AttentionArgs a{};
-        a.q = c->q;
-        a.q_bf16 = false;
+        a.q = nullptr;
+        a.bf16_io = false;
         a.out = c->ctx;
-        a.out_kind = 0;
+        a.fuse.qkv = c->qkv;
+        a.fuse.q_norm = L.q_norm;
+        a.fuse.k_norm = L.k_norm;
+        a.fuse.freq = m->freq;
+        a.fuse.eps = cfg.rms_eps;
         a.tables = c->kv->page_ptrs;
         a.table_stride = 0;
         a.ctx = c->state + 1;
@@ -335,6 +236,8 @@ static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx,
         a.max_ctx = max_ctx;
         a.partials = c->attn_partials;
         a.partial_floats = c->attn_partial_floats;
+        a.counters = c->attn_counters;
+        a.counter_count = attention_counters(1, CHUNK, cfg.heads);
         a.bytes_hint = (double)host_ctx * 2 * kvd * kv_elem_bytes(c->kv->format) + 2.0 * n * qd * 4;
         launch_attention(g, a);
         GemvIn ctx_in;
@@ -490,7 +393,6 @@ marin_status marin_qwen3_cache_new(marin_qwen3 *m, size_t capacity, marin_kv_for
             const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd();
             c->hidden = (float *)g->alloc(CHUNK * H * 4, true);
             c->qkv = (float *)g->alloc(CHUNK * (qd + 2 * kvd) * 4, true);
-            c->q = (float *)g->alloc(CHUNK * qd * 4, true);
             c->logits = (float *)g->alloc(cfg.vocab * 4, true);
             c->ctx = (float *)g->alloc(CHUNK * qd * 4, true);
             c->act = (float *)g->alloc(CHUNK * cfg.ffn * 4, true);
@@ -501,6 +403,7 @@ marin_status marin_qwen3_cache_new(marin_qwen3 *m, size_t capacity, marin_kv_for
             c->tokens_cap = std::max<size_t>(capacity, 1);
             c->attn_partial_floats = attention_partial_floats(1, CHUNK, cfg.heads, cfg.head_dim, capacity, g->cu_count);
             c->attn_partials = (float *)g->alloc(c->attn_partial_floats * 4, false);
+            c->attn_counters = (uint32_t *)g->alloc(attention_counters(1, CHUNK, cfg.heads) * 4, true);
         } catch (...) {
             marin_qwen3_cache_free(c.release());
             throw;
@@ -515,8 +418,8 @@ void marin_qwen3_cache_free(marin_qwen3_cache *c) {
     (void)hipStreamSynchronize(g->stream);
     free_cache_graph(c);
     marin_kv_free(c->kv);
-    for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->q, (void *)c->logits, (void *)c->ctx, (void *)c->act,
-                    (void *)c->best, (void *)c->ids, (void *)c->state, (void *)c->attn_partials,
+    for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->logits, (void *)c->ctx, (void *)c->act,
+                    (void *)c->best, (void *)c->ids, (void *)c->state, (void *)c->attn_partials, (void *)c->attn_counters,
                     (void *)c->tokens_out})
         g->release(p);
     delete c;

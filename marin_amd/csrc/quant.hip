@@ -93,7 +93,8 @@ void launch_gemv_valu(marin_gpu *g, const marin_quant_matrix *w, const float *x,
 // out[t][i] = code * scale of row ids[t] (quant.cu:209-214): one block per token.
 template <typename ST>
 __global__ void embed_q8_kernel(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
-                                const uint32_t *__restrict__ ids, float *__restrict__ out, int cols, int group) {
+                                const uint32_t *__restrict__ ids, float *__restrict__ out, int cols, int group,
+                                bool windowed) {
     const size_t row = ids[blockIdx.x];
     const int groups = cols / group;
     const ST *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
@@ -101,7 +102,7 @@ __global__ void embed_q8_kernel(const uint8_t *__restrict__ codes, const ST *__r
         float s;
         if constexpr (sizeof(ST) == 4) s = srow[(i / group) * 16];
         else s = __uint_as_float((unsigned)srow[(i / group) * 16] << 16);
-        out[(size_t)blockIdx.x * cols + i] = (float)(int8_t)codes[row * cols + i] * s;
+        out[(size_t)blockIdx.x * cols + i] = (float)(int8_t)codes[code_offset(row, i, cols, windowed, 16)] * s;
     }
 }
 
@@ -109,10 +110,10 @@ void launch_embed_q8(marin_gpu *g, const marin_quant_matrix *w, const uint32_t *
     if (!n) return;
     if (w->bf16_scales)
         embed_q8_kernel<uint16_t><<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(
-            w->codes, (const uint16_t *)w->scales, ids, out, (int)w->cols, (int)w->group);
+            w->codes, (const uint16_t *)w->scales, ids, out, (int)w->cols, (int)w->group, w->windowed);
     else
         embed_q8_kernel<float><<<dim3((unsigned)n), dim3(256), 0, g->stream>>>(
-            w->codes, (const float *)w->scales, ids, out, (int)w->cols, (int)w->group);
+            w->codes, (const float *)w->scales, ids, out, (int)w->cols, (int)w->group, w->windowed);
     g->launched();
 }
 
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(256) void synth_quantize_kernel(uint8_t *__restrict
             const float qf = roundf(v[k] / scale);
             code = (int)fminf(fmaxf(qf, -127.0f), 127.0f);
         }
-        codes[dst * cols + (size_t)gi * group + i] = (uint8_t)(int8_t)code;
+        codes[code_offset(dst, (size_t)gi * group + i, cols, true, 16)] = (uint8_t)(int8_t)code;
     }
     if (lane == 0) scales[(dst / 16) * (size_t)groups * 16 + (size_t)gi * 16 + (dst % 16)] = scale;
 }
@@ -180,6 +181,7 @@ void launch_synth_quantize(marin_gpu *g, marin_quant_matrix *w, uint64_t seed, u
                            size_t src_rows, size_t dst_row0, size_t dst_row_step) {
     if (w->bits != 8 || w->bf16_scales) throw Error(MARIN_UNSUPPORTED, "synthetic matrices are int8 with f32 scales");
     if (w->group > 256) unsupported("synthetic group size", 256, w->group);
+    if (!w->windowed) unsupported("synthetic matrix layout (group and columns multiples of 64)", 64, w->group);
     // Same mixing as or_synth_bf16: base = splitmix64(seed ^ splitmix64(stream + constant)).
     auto mix = [](uint64_t x) {
         x += 0x9E3779B97F4A7C15ull;
@@ -216,6 +218,7 @@ marin_quant_matrix *new_quant_matrix(marin_gpu *g, size_t rows, size_t cols, int
     m->group = group;
     m->bf16_scales = bf16;
     m->rows_padded = (rows + ROW_PAD - 1) / ROW_PAD * ROW_PAD;
+    m->windowed = group % 64 == 0 && cols % 64 == 0;
     try {
         m->codes = (uint8_t *)g->alloc(mul(m->rows_padded, m->row_bytes(), "quantized codes") + 16, true);
         m->scales = g->alloc(mul(mul(m->rows_padded, m->groups(), "quantization scales"), bf16 ? 2 : 4,
@@ -261,20 +264,26 @@ void upload_rows(marin_quant_matrix *m, const uint8_t *codes_in, const void *sca
         repack_int4(codes_in, repacked.data(), repacked.size());
         codes = repacked.data();
     }
-    // Codes: contiguous when the rows land contiguously, else row by row on the host side.
-    std::vector<uint8_t> code_rows;
-    if (dst_row_step == 1) {
-        g->upload(m->codes + dst_row0 * rb, codes, src_rows * rb);
-    } else {
-        // Interleave into a host copy of the destination range, then one upload.
-        const size_t last = dst_row0 + (src_rows - 1) * dst_row_step;
-        const size_t span = last - dst_row0 + 1;
-        code_rows.resize(span * rb);
-        g->download(code_rows.data(), m->codes + dst_row0 * rb, span * rb);
-        for (size_t r = 0; r < src_rows; ++r)
-            std::memcpy(&code_rows[r * dst_row_step * rb], codes + r * rb, rb);
-        g->upload(m->codes + dst_row0 * rb, code_rows.data(), span * rb);
+    // Codes: rebuild the 16-row tiles the rows touch on the host (rows of a tile are contiguous in both layouts),
+    // then one upload.
+    const size_t last_row = dst_row0 + (src_rows - 1) * dst_row_step;
+    const size_t ct0 = dst_row0 / 16, ct1 = last_row / 16 + 1;
+    const size_t tile_bytes = 16 * rb, cb = code_chunk(m->bits);
+    std::vector<uint8_t> code_tiles((ct1 - ct0) * tile_bytes);
+    const bool whole = dst_row_step == 1 && dst_row0 % 16 == 0 && (src_rows % 16 == 0 || last_row + 1 >= m->rows);
+    if (!whole) g->download(code_tiles.data(), m->codes + ct0 * tile_bytes, code_tiles.size());
+    for (size_t r = 0; r < src_rows; ++r) {
+        const size_t dst = dst_row0 + r * dst_row_step;
+        const uint8_t *src = codes + r * rb;
+        uint8_t *tile = code_tiles.data() + (dst / 16 - ct0) * tile_bytes;
+        if (!m->windowed) {
+            std::memcpy(tile + (dst % 16) * rb, src, rb);
+        } else {
+            for (size_t b0 = 0; b0 < rb; b0 += cb)
+                std::memcpy(tile + code_offset(dst % 16, b0, rb, true, cb), src + b0, cb);
+        }
     }
+    g->upload(m->codes + ct0 * tile_bytes, code_tiles.data(), code_tiles.size());
     // Scales: rebuild the tiles the rows touch on the host, then upload them.
     const size_t last = dst_row0 + (src_rows - 1) * dst_row_step;
     const size_t t0 = dst_row0 / 16, t1 = last / 16 + 1;

@@ -3,9 +3,15 @@
 
 #include "common.hpp"
 
-// Device layout of a quantized matrix (the reference keeps Quantized's layout, crates/cuda/src/quant.rs:16-23; this
-// backend keeps the codes byte for byte but stores the scales tiled for the MFMA product):
-//  codes  [rows_padded][row_bytes]   int8 two's complement, or int4 pairs (even column low nibble, +8)
+// Device layout of a quantized matrix (the reference keeps Quantized's row-major layout, crates/cuda/src/quant.rs:16-23;
+// this backend keeps every code byte but places them for the matrix-core product):
+//  codes, windowed (group and columns multiples of 64, the matrix-core product's matrices):
+//         [rows_padded/16 tiles][cols/64 windows][64 lanes][CB bytes], CB = 16 (int8) or 8 (int4). Lane l of a
+//         window holds row 16 * tile + l % 16, columns 64 * window + 16 * (l / 16) .. + 16: exactly the A operand of
+//         one v_mfma_i32_16x16x64_i8, so every wave load is one contiguous 1 KiB (512 B) run of HBM.
+//  codes, row-major (other groups): [rows_padded][row_bytes].
+//  int4 bytes: each 4-byte word holds 8 consecutive columns, columns 0-3 in the low nibbles and 4-7 in the high
+//         nibbles (stored value code + 8).
 //  scales [rows_padded/16][groups][16]  f32 or bf16: the 16 rows of a tile side by side for each group, so a lane
 //         reads the scales of its four output rows with one 16-byte (8-byte) load.
 // Rows past `rows` up to the next multiple of 64 are zero codes with zero scales.
@@ -14,6 +20,7 @@ struct marin_quant_matrix {
     size_t rows = 0, cols = 0, group = 0, rows_padded = 0;
     int bits = 8;
     bool bf16_scales = false;
+    bool windowed = false;
     uint8_t *codes = nullptr;
     void *scales = nullptr;
     size_t groups() const { return cols / group; }
@@ -21,6 +28,14 @@ struct marin_quant_matrix {
 };
 
 namespace marin {
+
+// Byte offset of byte `b` of row `row` (in the row-major device row, int4 already repacked) in the codes.
+__host__ __device__ inline size_t code_offset(size_t row, size_t b, size_t row_bytes, bool windowed, size_t cb) {
+    if (!windowed) return row * row_bytes + b;
+    const size_t j = b / cb;  // 16-column chunk of the row
+    return (row >> 4) * 16 * row_bytes + (j >> 2) * 64 * cb + ((j & 3) * 16 + (row & 15)) * cb + b % cb;
+}
+inline size_t code_chunk(int bits) { return bits == 8 ? 16 : 8; }
 
 constexpr size_t ROW_PAD = 64;
 

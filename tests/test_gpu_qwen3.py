@@ -135,5 +135,6 @@ def test_profiled_step_accounts_every_launch(gpu):
     p = model.profile_step(c)
     L = g["shape"]["layers"]
     assert p["gemv_launches"] == 4 * L + 1
-    assert p["attention_launches"] == 2 * L
+    # one attention launch per layer: q/k norm, RoPE, the cache store and the chunk merge happen inside it
+    assert p["attention_launches"] == L
     assert p["gemv_bytes"] > 0 and p["gemv_seconds"] > 0 and p["step_seconds"] >= p["gemv_seconds"]
