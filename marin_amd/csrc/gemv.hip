@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "gemv.hpp"
 
@@ -456,7 +457,8 @@ void launch_gemv(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     if (!tokens) return;
     if (tokens > GEMV_TOKENS) unsupported("tokens per product", GEMV_TOKENS, tokens);
     if (!gemv_supported(w)) unsupported("matrix-core product layout (group and columns multiples of 64)", 64, w->group);
-    if (w->bf16_scales) launch_st<uint16_t>(g, w, in, out, tokens);
+    if (tokens == 1 && gemv_decode_supported(w) && !getenv("MARIN_OLD_DECODE")) launch_gemv_decode(g, w, in, out);
+    else if (w->bf16_scales) launch_st<uint16_t>(g, w, in, out, tokens);
     else launch_st<float>(g, w, in, out, tokens);
     // algorithmic bytes: codes + scales once, activations and outputs once
     const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;

@@ -1,0 +1,418 @@
+// The one-token quantized product (decode), built for latency on CDNA4.
+//
+// Same arithmetic as the multi-token matrix-core product (codes are the A operand of v_mfma_i32_16x16x64_i8,
+// activations become exact signed 8-bit limbs in the B columns, int32 sums per group scaled once per group), with a
+// schedule cut down to what one token needs:
+//  - every wave owns a fixed slice of the columns (whole groups) for the whole launch, so it builds the limbs of its
+//    slice once, into LDS, and reuses them for every 16-row tile it visits;
+//  - the power of two that scales the activations into 30-bit integers is chosen per group of columns (from the
+//    group's largest magnitude), not per row, so no block-wide maximum is needed; it is folded into the group's
+//    weight scale;
+//  - a register ring of code windows runs across tile ends, so the next tile's codes are in flight while a tile's
+//    sums are reduced; the reduction is one LDS exchange and one barrier per tile (double-buffered);
+//  - the launch is persistent: blocks take tiles b, b + grid, ... with a grid sized to what stays resident.
+// The prologue (activation loads, RMSNorm statistic, limbs) runs while the first windows of codes are in flight.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "gemv.hpp"
+
+namespace marin {
+
+namespace {
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#ifndef DECODE_WAVES
+#define DECODE_WAVES 8
+#endif
+#ifndef DECODE_RING
+#define DECODE_RING 8
+#endif
+constexpr int DW = DECODE_WAVES;   // waves per block
+constexpr int RING = DECODE_RING;  // code windows in flight per wave
+#ifndef DECODE_BPC
+#define DECODE_BPC 2
+#endif
+constexpr int DECODE_BLOCKS_PER_CU = DECODE_BPC;  // resident blocks the persistent grid aims at per compute unit
+
+// Lane permutations inside rows of 16 lanes (DPP): 0xB1 swaps neighbours, 0x4E swaps pairs, 0x141 mirrors each
+// half row of 8 lanes.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+__device__ __forceinline__ int total_key(float v) {
+    const int b = __float_as_int(v);
+    return b ^ (int)(((unsigned)(b >> 31)) >> 1);
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+template <typename ST>
+__device__ __forceinline__ floatx4 scales4(const ST *p) {
+    if constexpr (sizeof(ST) == 4) {
+        return *reinterpret_cast<const floatx4 *>(p);
+    } else {
+        const uint2 s = *reinterpret_cast<const uint2 *>(p);
+        return (floatx4){__uint_as_float(s.x << 16), __uint_as_float(s.x & 0xffff0000u), __uint_as_float(s.y << 16),
+                         __uint_as_float(s.y & 0xffff0000u)};
+    }
+}
+
+}  // namespace
+
+// Timeline stamps for tuning (built only with -DDECODE_TRACE): per block, the 100 MHz wall clock at entry (0),
+// activation loads issued (1), ring issued (2), limbs built (4), after the prologue barrier (5), first tile done (6)
+// and exit (7).
+#ifdef DECODE_TRACE
+__device__ unsigned long long decode_trace[4096 * 8];
+#define TRACE(k) do { if (threadIdx.x == 0 && blockIdx.x < 4096) decode_trace[blockIdx.x * 8 + (k)] = wall_clock64(); } while (0)
+#else
+#define TRACE(k) do { } while (0)
+#endif
+
+// BITS 8 or 4; WG = 64-column windows per quantization group (group = 64 * WG); SM = windows per wave per tile
+// (wave w owns windows [w * SM, (w + 1) * SM) of every row; waves past the last window hold no groups); ST = scale
+// type (float or bf16 bits).
+//
+// Every global load is unconditional (out-of-range addresses are clamped), and the activation loads are issued
+// before the code ring: the memory counter the wave waits on then lets the activations arrive without draining the
+// ring, and the ring stays exactly RING windows deep through the main loop.
+template <int BITS, int WG, int SM, typename ST>
+__global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
+                                                       GemvIn in, GemvOut out, int rows, int cols, int tiles) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    TRACE(0);
+    constexpr int S = SM;
+    constexpr int CB = BITS == 8 ? 16 : 8;  // code bytes per lane per window
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, q = lane >> 4;
+    const int windows = cols >> 6;
+    const int groups = windows / WG;
+    const size_t tile_bytes = (size_t)16 * (BITS == 8 ? cols : cols / 2);
+
+    // LDS: limbs [DW][S][4][64] bytes | down-scale per group [groups] f32 | int4 offsets [groups][4] i32 |
+    //      wave sums [2][DW][16] f32 | sum of squares [DW] f32
+    int8_t *limbs = reinterpret_cast<int8_t *>(lds);
+    float *gdown = reinterpret_cast<float *>(lds + (size_t)DW * S * 256);
+    const int gpad = (groups + 3) & ~3;  // keeps the wave sums 16-byte aligned
+    int *goff = reinterpret_cast<int *>(gdown + gpad);
+    float *red = reinterpret_cast<float *>(goff + (BITS == 4 ? gpad * 4 : 0));
+    float *ssq = red + 2 * DW * 16;
+
+    const int w0 = wave * S;  // first window of this wave's slice
+    const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int items = my_tiles * S;
+
+    // ---- activations of the slice first. In round r, lane L holds the 16 consecutive columns
+    // 64 w0 + 1024 r + 16 L .. + 16, i.e. quarter L % 4 of window r * 16 + L / 4 of the slice: exactly what the B
+    // operand of that window needs, so the lane builds all four limbs of its columns and stores each as 16 bytes.
+    // Four 16-byte loads per round in every mode (bf16 rows use the first two), and the norm weights always loaded
+    // (the activation address stands in when there is no norm), so no branch joins loaded values before the ring
+    // is issued: waiting for them then never drains the ring.
+    constexpr int R = (S + 15) / 16;
+    const bool norm = in.mode == IN_NORM, bf = in.mode == IN_BF16;
+    const unsigned char *xb = reinterpret_cast<const unsigned char *>(in.x);
+    u32x4 xr[R][4], nr[R][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int cb = min(w0 * 64 + r * 1024 + 16 * lane, cols - 16);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const size_t xo = bf ? (size_t)cb * 2 + 16 * (v & 1) : (size_t)cb * 4 + 16 * v;
+            xr[r][v] = *reinterpret_cast<const u32x4 *>(xb + xo);
+            nr[r][v] = *reinterpret_cast<const u32x4 *>(norm ? reinterpret_cast<const unsigned char *>(in.norm + cb) + 16 * v
+                                                              : xb + xo);
+        }
+    }
+
+    TRACE(1);
+    // ---- the ring: item i = (tile blockIdx + (i / S) * grid, window w0 + i % S)
+    typedef typename std::conditional<BITS == 8, u32x4, u32x2>::type Raw;
+    Raw ring[RING];
+    floatx4 sring[RING / WG];
+    auto load_item = [&](int i, int slot) {
+        const int t = (int)blockIdx.x + (i / S) * (int)gridDim.x;
+        const int w = min(w0 + i % S, windows - 1);
+        const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane;
+        if constexpr (BITS == 8) ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+        else ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+        if (slot % WG == 0) sring[slot / WG] = scales4(scales + ((size_t)t * groups + w / WG) * 16 + 4 * q);
+    };
+    const int last = items > 0 ? items - 1 : 0;
+#pragma unroll
+    for (int j = 0; j < RING; ++j) load_item(min(j, last), j);
+    TRACE(2);
+
+    // ---- prologue: RMSNorm statistic (the waves' slices cover the row once), then this wave's limbs
+    float xv[R][16];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            if (bf) {
+                const uint32_t wd = xr[r][e / 8][(e / 2) % 4];
+                xv[r][e] = __uint_as_float((e & 1) ? (wd & 0xffff0000u) : (wd << 16));
+            } else {
+                xv[r][e] = __uint_as_float(xr[r][e / 4][e % 4]);
+            }
+        }
+    }
+    auto in_slice = [&](int r) {  // this lane's columns lie in the slice and in the row
+        const int wl = r * 16 + lane / 4;
+        return wl < S && w0 + wl < windows;
+    };
+    float rs = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (in_slice(r))
+#pragma unroll
+                for (int e = 0; e < 16; ++e) ss += xv[r][e] * xv[r][e];
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) ssq[wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < DW; ++w) total += ssq[w];
+        rs = 1.0f / sqrtf(total / (float)cols + in.eps);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int wl = r * 16 + lane / 4;
+        const bool valid = in_slice(r);
+        float v[16];
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float x = xv[r][e];
+            if (norm) x = x * rs * __uint_as_float(nr[r][e / 4][e % 4]);
+            v[e] = x;
+            mx = fmaxf(mx, fabsf(x));
+        }
+        // the group's largest magnitude: its 4 WG lanes are consecutive
+        mx = fmaxf(mx, dpp_f<0xB1>(mx));  // lanes xor 1
+        mx = fmaxf(mx, dpp_f<0x4E>(mx));  // lanes xor 2
+        if constexpr (WG == 2) mx = fmaxf(mx, dpp_f<0x141>(mx));  // the other quad of the 8 lanes
+        int sh = 0;
+        if (mx > 0.0f && mx < INFINITY) {
+            int e;
+            (void)frexpf(mx, &e);
+            sh = 30 - e;  // largest magnitude lands in [2^29, 2^30)
+            sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+        }
+        const float up = ldexpf(1.0f, sh);
+        u32x4 pk[4];
+        int lsum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int l = 0; l < 4; ++l) pk[l] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            int xi = __float2int_rn(v[e] * up);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int lb = l == 3 ? xi : (int)(int8_t)(xi & 0xff);
+                pk[l][e / 4] |= ((uint32_t)lb & 0xffu) << (8 * (e % 4));
+                lsum[l] += lb;
+                xi = (xi - lb) >> 8;
+            }
+        }
+        if (valid) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l)
+                *reinterpret_cast<u32x4 *>(limbs + ((size_t)(wave * S + wl) * 4 + l) * 64 + 16 * (lane & 3)) = pk[l];
+        }
+        const int g = (w0 + wl) / WG;
+        if (valid && (lane & (4 * WG - 1)) == 0) gdown[g] = ldexpf(1.0f, -sh);
+        if constexpr (BITS == 4) {
+            // stored nibbles are code + 8: the group's sum of each limb column, times 8, comes off the sums
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                int sm = lsum[l];
+                sm += dpp_i<0xB1>(sm);
+                sm += dpp_i<0x4E>(sm);
+                if constexpr (WG == 2) sm += dpp_i<0x141>(sm);
+                if (valid && (lane & (4 * WG - 1)) == 0) goff[g * 4 + l] = 8 * sm;
+            }
+        }
+    }
+    TRACE(4);
+    __syncthreads();
+    TRACE(5);
+
+    floatx4 total = (floatx4){0.f, 0.f, 0.f, 0.f};
+    floatx4 gsc = total;
+    int4v acc = (int4v){0, 0, 0, 0};
+    unsigned long long best = 0ull;
+    int tile_n = 0;
+    for (int base = 0; base < items; base += RING) {
+#pragma unroll
+        for (int j = 0; j < RING; ++j) {
+            const int i = base + j;
+            const Raw cur = ring[j];
+            if (j % WG == 0) gsc = sring[j / WG];  // the slot is refilled below, before the group's last window
+            load_item(min(i + RING, last), j);
+            if (i >= items) continue;
+            const int wl = i % S;      // window inside the slice
+            const int w = w0 + wl;     // window of the row
+            int4v b = (int4v){0, 0, 0, 0};
+            if (c < 4 && w < windows) b = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + c) * 64 + 16 * q);
+            int4v a;
+            if constexpr (BITS == 8) {
+                a = __builtin_bit_cast(int4v, cur);
+            } else {
+                a = (int4v){(int)(cur.x & 0x0f0f0f0fu), (int)((cur.x >> 4) & 0x0f0f0f0fu), (int)(cur.y & 0x0f0f0f0fu),
+                            (int)((cur.y >> 4) & 0x0f0f0f0fu)};
+            }
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+            if (j % WG == WG - 1) {
+                // end of a group: one conversion, scaled by weight scale x 2^-shift of the group
+                if (w < windows) {
+                    const int g = w / WG;
+                    if constexpr (BITS == 4) {
+                        const int off = c < 4 ? goff[g * 4 + c] : 0;
+                        acc -= (int4v){off, off, off, off};
+                    }
+                    const float d = gdown[g];
+                    const floatx4 f = (floatx4){(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
+                    total += f * (gsc * d);
+                }
+                acc = (int4v){0, 0, 0, 0};
+            }
+            if (wl == S - 1) {
+                // ---- end of a tile: limbs weighted 2^(8c) and summed over c, then over the waves
+                float r4[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float v = c < 4 ? total[k] * (c == 0 ? 1.0f : c == 1 ? 256.0f : c == 2 ? 65536.0f : 16777216.0f)
+                                    : 0.0f;
+                    v += __shfl_xor(v, 1);
+                    v += __shfl_xor(v, 2);
+                    r4[k] = v;
+                }
+                float *rb = red + (tile_n & 1) * DW * 16;
+                if (c == 0) *reinterpret_cast<float4 *>(rb + wave * 16 + 4 * q) = make_float4(r4[0], r4[1], r4[2], r4[3]);
+                total = (floatx4){0.f, 0.f, 0.f, 0.f};
+                __syncthreads();
+                if (tile_n == 0) TRACE(6);
+                if (wave == 0 && lane < 16) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int ww = 0; ww < DW; ++ww) v += rb[ww * 16 + lane];
+                    const int t = (int)blockIdx.x + tile_n * (int)gridDim.x;
+                    const int row = t * 16 + lane;
+                    if (out.mode == OUT_SILU) {
+                        const float upv = __shfl_xor(v, 1);
+                        if ((lane & 1) == 0 && row < rows)
+                            reinterpret_cast<float *>(out.y)[row >> 1] = silu_f(v) * upv;
+                    } else if (row < rows) {
+                        if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[row] = v;
+                        else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[row] += v;
+                        else {
+                            const unsigned uu = __float_as_uint(v);
+                            reinterpret_cast<uint16_t *>(out.y)[row] = (uint16_t)(
+                                (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
+                                                                 : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+                        }
+                        if (out.argmax) {
+                            // largest under f32's total order, lowest row on ties (sampler/src/lib.rs:40-48)
+                            const unsigned long long key =
+                                (unsigned long long)((unsigned)total_key(v) ^ 0x80000000u) << 32 |
+                                (unsigned long long)(0xffffffffu - (unsigned)row);
+                            best = key > best ? key : best;
+                        }
+                    }
+                }
+                ++tile_n;
+            }
+        }
+    }
+    TRACE(7);
+    if (out.argmax && wave == 0) {
+        for (int o = 8; o > 0; o >>= 1) {
+            const unsigned long long other = __shfl_xor(best, o);
+            best = other > best ? other : best;
+        }
+        if (lane == 0 && best) atomicMax(out.argmax, best);
+    }
+}
+
+// Windows per wave per tile for a row of `windows` 64-column windows: the smallest instantiated width whose DW
+// slices cover the row, 0 when none does.
+static int slice_windows(int windows) {
+    for (int sm : {4, 8, 24})
+        if (DW * sm >= windows) return sm;
+    return 0;
+}
+
+template <int BITS, int WG, int SM, typename ST>
+static void launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+    const int windows = (int)(w->cols / 64);
+    const int groups = windows / WG;
+    const int tiles = (int)(w->rows_padded / 16);
+    const size_t gpad = (size_t)((groups + 3) & ~3);
+    const size_t lds = (size_t)DW * SM * 256 + gpad * 4 + (BITS == 4 ? gpad * 16 : 0) + (size_t)(2 * DW * 16 + DW) * 4;
+    auto kern = gemv_decode<BITS, WG, SM, ST>;
+    if (lds > 64 * 1024) {
+        if (lds > 160 * 1024) unsupported("decode product shared memory (KiB)", 160, lds / 1024);
+        HIP_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    }
+    int resident = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * DW, lds) != hipSuccess || resident < 1)
+        resident = 1;
+    const int cu = std::max(g->cu_count, 1);
+    const int blocks = std::min(tiles, std::min(resident, DECODE_BLOCKS_PER_CU) * cu);
+    kern<<<dim3((unsigned)blocks), dim3(64 * DW), lds, g->stream>>>(w->codes, (const ST *)w->scales, in, out,
+                                                                    (int)w->rows, (int)w->cols, tiles);
+}
+
+template <int BITS, int WG, typename ST>
+static void launch_decode_sm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+    switch (slice_windows((int)(w->cols / 64))) {
+        case 4: launch_decode_t<BITS, WG, (WG > 4 ? WG : 4), ST>(g, w, in, out); break;
+        case 8: launch_decode_t<BITS, WG, 8, ST>(g, w, in, out); break;
+        default: launch_decode_t<BITS, WG, 24, ST>(g, w, in, out); break;
+    }
+}
+
+template <typename ST>
+static void launch_decode_st(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+    const bool wg2 = w->group == 128;
+    if (w->bits == 8) {
+        if (wg2) launch_decode_sm<8, 2, ST>(g, w, in, out);
+        else launch_decode_sm<8, 1, ST>(g, w, in, out);
+    } else {
+        if (wg2) launch_decode_sm<4, 2, ST>(g, w, in, out);
+        else launch_decode_sm<4, 1, ST>(g, w, in, out);
+    }
+}
+
+bool gemv_decode_supported(const marin_quant_matrix *w) {
+    return gemv_supported(w) && (w->group == 64 || w->group == 128) && slice_windows((int)(w->cols / 64)) > 0;
+}
+
+#ifdef DECODE_TRACE
+extern "C" void marin_decode_trace_read(unsigned long long *host) {
+    (void)hipMemcpyFromSymbol(host, HIP_SYMBOL(decode_trace), sizeof(decode_trace));
+}
+#endif
+
+void launch_gemv_decode(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+    if (w->bf16_scales) launch_decode_st<uint16_t>(g, w, in, out);
+    else launch_decode_st<float>(g, w, in, out);
+}
+
+}  // namespace marin
