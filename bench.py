@@ -8,8 +8,13 @@ accumulation). Weights are random-init N(0, 0.02) generated and quantized on the
 is 4096 uniform random ids, prefilled before timing. The timed region is exactly K steps between two stream
 synchronizations, with every input already resident in HBM.
 
-One JSON line goes to stdout. `roofline` comes from event-profiled decode steps run right after the timed region
-(an event after every launch; the quantized products' algorithmic bytes over their summed durations). `cpu_baseline`
+One JSON line goes to stdout. `roofline` comes from measurements right after the timed region: profiled decode
+steps tag every product and attention launch with its kernel instantiation and algorithmic bytes; then, per kernel,
+one decode pass's launches of that kernel alone are captured into a HIP graph and replayed between two events on the
+stream they run on, which gives its mean launch duration (kernel time plus the graph's gap to the next launch). The
+dominant kernel is the product instantiation with the most time per step; `achieved` is its algorithmic bytes per
+launch over its mean launch duration (`kernels` lists every instantiation the same way). `traffic` is that kernel's HBM bytes per launch
+from the committed rocprofv3 counter runs (profiles/traffic.json), when present. `cpu_baseline`
 times the CPU oracle (oracle/marin_oracle.c, a C restatement of Marin's single-threaded int8 decode GEMV and
 attention) on one core over a bounded sample of the same token's work.
 """
@@ -80,6 +85,11 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--no-timing", action="store_true",
+                    help="skip the per-kernel graph timing (for rocprofv3 counter runs, which only need the decode "
+                         "dispatches); mean launch durations then come from the profiled steps' events")
+    ap.add_argument("--probe-copy", type=float, default=0.0, metavar="MB",
+                    help="only run the bandwidth probe: copies of MB megabytes (for counter calibration), then exit")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's kernels one by one instead of replaying a HIP graph (for tracers)")
     args = ap.parse_args()
@@ -92,6 +102,13 @@ def main() -> int:
 
     import marin_amd as m
     from marin_amd.qwen3 import SHAPES, Qwen3, weight_bytes
+
+    if args.probe_copy:
+        nbytes = int(args.probe_copy * 1e6) // 16 * 16
+        sec = m.Gpu().probe_copy(nbytes, 50)
+        print(json.dumps({"probe": "copy", "bytes": nbytes, "seconds": sec,
+                          "GBps_read_plus_write": round(2 * nbytes / sec / 1e9, 1)}), flush=True)
+        return 0
 
     shape = SHAPES["qwen3-8b"]
     fmt = {"f32": m.KvFormat.F32, "f16": m.KvFormat.F16, "bf16": m.KvFormat.BF16}[args.kv]
@@ -124,19 +141,47 @@ def main() -> int:
     print(f"[bench] {args.steps} steps in {wall * 1e3:.1f} ms (events {gpu_s * 1e3:.1f} ms): {tok_s:.1f} tok/s",
           file=sys.stderr, flush=True)
 
-    profs = [model.profile_step(cache) for _ in range(args.profile_steps)]
-    gemv_s = sum(p["gemv_seconds"] for p in profs)
-    gemv_b = sum(p["gemv_bytes"] for p in profs)
-    attn_s = sum(p["attention_seconds"] for p in profs)
-    attn_b = sum(p["attention_bytes"] for p in profs)
-    step_s = sum(p["step_seconds"] for p in profs) / len(profs)
-    gemv_gbps = gemv_b / gemv_s / 1e9
-    attn_gbps = attn_b / attn_s / 1e9 if attn_s else 0.0
-    launches = profs[0]["gemv_launches"]
-    print(f"[bench] profiled step {step_s * 1e3:.3f} ms: gemv {gemv_s / len(profs) * 1e3:.3f} ms "
-          f"({gemv_gbps:.0f} GB/s over {launches} launches), attention {attn_s / len(profs) * 1e3:.3f} ms "
-          f"({attn_gbps:.0f} GB/s), other {sum(p['other_seconds'] for p in profs) / len(profs) * 1e3:.3f} ms",
-          file=sys.stderr, flush=True)
+    # Per-launch durations, each product and attention launch bracketed by its own two events on the stream it runs
+    # on (one decode step per profiled step, launched eagerly so the events can sit between the kernels).
+    recs = []
+    for _ in range(args.profile_steps):
+        recs += model.profile_launches(cache)
+    kernels = {}
+    for kind, name, nbytes, sec in recs:
+        if kind == 0:
+            continue
+        k = kernels.setdefault(name, {"kind": "product" if kind == 1 else "attention", "launches": 0, "bytes": 0.0,
+                                      "seconds": 0.0})
+        k["launches"] += 1
+        k["bytes"] += nbytes
+        k["seconds"] += sec
+    steps_p = args.profile_steps
+    summary = {}
+    for name, k in kernels.items():
+        # mean launch duration: graph replays of one pass's launches of this kernel alone, between two events
+        if args.no_timing:
+            sec, n = k["seconds"] / k["launches"], k["launches"] // steps_p
+        else:
+            sec, n = model.time_kernel(cache, name, reps=20)
+        summary[name] = {"kind": k["kind"], "launches_per_step": k["launches"] // steps_p,
+                         "bytes_per_launch": round(k["bytes"] / k["launches"]),
+                         "mean_launch_us": round(sec * 1e6, 3),
+                         "GBps": round(k["bytes"] / k["launches"] / sec / 1e9, 1),
+                         "us_per_step": round(sec * n * 1e6, 1),
+                         "eager_event_us": round(k["seconds"] / k["launches"] * 1e6, 3)}
+    dom = max((n for n in summary if summary[n]["kind"] == "product"), key=lambda n: summary[n]["us_per_step"])
+    dk = summary[dom]
+    gemv_b = sum(k["bytes"] for k in kernels.values() if k["kind"] == "product") / steps_p
+    attn_b = sum(k["bytes"] for k in kernels.values() if k["kind"] == "attention") / steps_p
+    for name, k in sorted(summary.items(), key=lambda kv: -kv[1]["us_per_step"]):
+        print(f"[bench] {name}: {k['launches_per_step']} launches/step, {k['mean_launch_us']:.2f} us each, "
+              f"{k['GBps']:.0f} GB/s, {k['us_per_step']:.0f} us/step", file=sys.stderr, flush=True)
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        t = json.load(open(tpath)).get("kernels", {}).get(dom)
+        if t:
+            traffic = t["hbm_bytes_per_launch"]
 
     line = {
         "metric": "decode tok/s Qwen3-8B-shape int8 bs=1; GEMV+attn HBM GB/s vs 8 TB/s peak",
@@ -155,12 +200,12 @@ def main() -> int:
                    "prompt": args.prompt, "batch": 1, "kv_format": args.kv, "layers": shape["layers"],
                    "hidden": shape["hidden"], "heads": shape["heads"], "kv_heads": shape["kv_heads"],
                    "ffn": shape["ffn"], "vocab": shape["vocab"], "group": shape["group"]},
-        "roofline": {"bound": "hbm", "kernel": "gemv_i8_mfma (all decode launches, byte-weighted)",
-                     "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "bytes_per_step": gemv_b / len(profs), "launches_per_step": launches},
-        "attention": {"achieved_GBps": round(attn_gbps, 1), "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
-                      "seconds_per_step": attn_s / len(profs)},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(dk["GBps"] / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "bytes_per_launch": dk["bytes_per_launch"], "mean_launch_us": dk["mean_launch_us"],
+                     "launches_per_step": dk["launches_per_step"]},
+        "kernels": summary,
+        "step_algorithmic_GBps": round((gemv_b + attn_b) / (wall / args.steps) / 1e9, 1),
         "weight_bytes_per_token": weight_bytes(shape),
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
         "gpu": info["name"],

@@ -3,7 +3,7 @@
  *
  * Every entry point mirrors a public item of the reference's `cuda` crate, the backend that crates/model and
  * crates/runtime call (cited per declaration as crates/cuda/src/<file>:<line>). A Rust crate `hip` that wraps these
- * functions with the same method names can stand in for `cuda` (see INTEGRATION.md in the repository root).
+ * functions with the same method names can stand in for `cuda`, published under that name to crates/model.
  *
  * Conventions (crates/cuda/src/error.rs:6-36, gpu.rs:68-76):
  *  - Every fallible call returns a marin_status. On failure the calling thread's last error (marin_last_error*) holds
@@ -247,6 +247,27 @@ typedef struct marin_step_profile {
     uint32_t gemv_launches, attention_launches, other_launches;
 } marin_step_profile;
 marin_status marin_qwen3_profile_step(marin_qwen3 *m, marin_qwen3_cache *c, marin_step_profile *out);
+/* Extension (measurement, the role of GpuProbe + Gpu::mark, model/src/qwen3/gpu_probe.rs, cuda/src/counters.rs:91-111):
+ * one decode step with events around every launch; the launches in order, `count` of them (at most `cap` written).
+ * kind: 0 other, 1 quantized product, 2 attention; seconds between the launch's own events (products and
+ * attention) or from the previous launch's event; name: the kernel instantiation as profilers print it. */
+typedef struct marin_launch_record {
+    uint32_t kind;
+    double bytes, seconds;
+    char name[96];
+} marin_launch_record;
+marin_status marin_qwen3_profile_launches(marin_qwen3 *m, marin_qwen3_cache *c, marin_launch_record *out,
+                                          size_t cap, size_t *count);
+/* Extension (measurement): one decode pass captured into a HIP graph with only the launches of kernel `name` (as
+ * marin_launch_record names it), replayed `reps` times between two events on the stream: mean seconds per launch
+ * (kernel time plus the graph's gap to the next launch) and launches per pass. The pass's matrices, inputs and
+ * outputs are the decode step's; it leaves the cache's activations (not its keys and values) unspecified. */
+marin_status marin_qwen3_time_kernel(marin_qwen3 *m, marin_qwen3_cache *c, const char *name, int reps,
+                                     double *seconds_per_launch, uint32_t *launches_per_pass);
+
+/* Extension (bandwidth probe, the role of cuda/src/probe.rs:145-314): `reps` device-to-device copies of `bytes`
+ * (a multiple of 16) through a plain streaming kernel; the mean seconds per copy. */
+marin_status marin_probe_copy(marin_gpu *gpu, size_t bytes, int reps, double *seconds);
 
 /* Extension: a rows x cols int8 matrix from the synthetic generator (seed, stream), N(0, std), quantized on the
  * device with the reference's rule (tensor/src/quant.rs:181-234); the oracle restates both bit for bit. */

@@ -314,6 +314,13 @@ class Gpu:
         check(lib.marin_quantized_synthetic(self._h, rows, cols, group, seed, stream, std, C.byref(h)))
         return DeviceQuantMatrix(h)
 
+    def probe_copy(self, nbytes: int, reps: int = 20) -> float:
+        """Mean seconds of one device-to-device copy of `nbytes` by a plain streaming kernel (extension; see
+        include/marin_hip.h)."""
+        sec = C.c_double()
+        check(lib.marin_probe_copy(self._h, nbytes, reps, C.byref(sec)))
+        return sec.value
+
     def embed_quant(self, table: DeviceQuantMatrix, ids, scratch: Tokens, out: Buffer) -> None:
         ids = np.ascontiguousarray(ids, np.uint32).ravel()
         check(lib.marin_embed_quant(self._h, table._h, ids.ctypes.data if ids.size else None, ids.size,

@@ -33,6 +33,10 @@ class StepProfileC(C.Structure):
         (n, C.c_uint32) for n in ("gemv_launches", "attention_launches", "other_launches")]
 
 
+class LaunchRecordC(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("bytes", C.c_double), ("seconds", C.c_double), ("name", C.c_char * 96)]
+
+
 class Qwen3ConfigC(C.Structure):
     _fields_ = [(n, sz) for n in ("layers", "hidden", "heads", "kv_heads", "head_dim", "ffn", "vocab")] + [
         ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("tie_embeddings", C.c_int), ("group", sz)]
@@ -113,6 +117,9 @@ SIGNATURES = {
     "marin_qwen3_generate": (st, [P, P, P, sz, sz, P]),
     "marin_qwen3_decode": (st, [P, P, sz, P]),
     "marin_qwen3_profile_step": (st, [P, P, C.POINTER(StepProfileC)]),
+    "marin_probe_copy": (st, [P, sz, C.c_int, C.POINTER(C.c_double)]),
+    "marin_qwen3_time_kernel": (st, [P, P, C.c_char_p, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint32)]),
+    "marin_qwen3_profile_launches": (st, [P, P, C.POINTER(LaunchRecordC), sz, C.POINTER(sz)]),
     "marin_quantized_synthetic": (st, [P, sz, sz, sz, C.c_uint64, C.c_uint64, C.c_double, PP]),
 }
 

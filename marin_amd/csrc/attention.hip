@@ -8,9 +8,11 @@
 // the same pass with an online softmax; the chunks of a row group are merged (log-sum-exp) by the last of them to
 // finish, in the same launch.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 
 #include "attention.hpp"
 
@@ -578,9 +580,18 @@ static int rows_per_block(const AttentionArgs &a) {
 
 template <int F, int LPP, bool VEC, bool BF16IO, int R, bool FUSE>
 static void launch_split(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
-    attention_split<F, LPP, VEC, BF16IO, R, FUSE, NWAVES><<<grid, dim3(64 * NWAVES), 0, g->stream>>>(
-        a.q, a.fuse, a.tables, a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk,
-        splits, scale, a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+    hipEvent_t t0, t1;
+    g->kernel_events(t0, t1);
+    auto kern = attention_split<F, LPP, VEC, BF16IO, R, FUSE, NWAVES>;
+    if (t0)
+        hipExtLaunchKernelGGL(kern, grid, dim3(64 * NWAVES), 0u, g->stream, t0, t1, 0u, a.q, a.fuse, a.tables,
+                              a.table_stride, a.ctx, a.geom, (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk,
+                              splits, scale, a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+    else
+        kern<<<grid, dim3(64 * NWAVES), 0, g->stream>>>(a.q, a.fuse, a.tables, a.table_stride, a.ctx, a.geom,
+                                                        (int)a.tokens, (int)a.heads, (int)a.kv_heads, chunk, splits,
+                                                        scale, a.partials, (int)(a.partial_floats * 4), a.counters,
+                                                        a.out);
 }
 
 template <int F, int LPP, bool VEC, int R>
@@ -636,13 +647,14 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     if (counters > a.counter_count) shape("attention chunk counters", counters, a.counter_count);
     // scores in the log2 domain: dot * (1/sqrt(hd)) * log2(e), weights 2^(s - max) with the hardware exp2
     const float scale = (float)(1.4426950408889634 / std::sqrt((double)a.geom.head_dim));
+    if (g->only && strcmp(g->only, "attention_split")) return;
     dim3 grid((unsigned)splits, (unsigned)(a.kv_heads * row_groups), (unsigned)a.batch);
     switch (a.geom.format) {
         case MARIN_KV_F32: launch_split_f<MARIN_KV_F32>(g, a, grid, chunk, splits, scale); break;
         case MARIN_KV_F16: launch_split_f<MARIN_KV_F16>(g, a, grid, chunk, splits, scale); break;
         default: launch_split_f<MARIN_KV_BF16>(g, a, grid, chunk, splits, scale); break;
     }
-    g->launched(marin_gpu::ATTENTION, a.bytes_hint);
+    g->launched(marin_gpu::ATTENTION, a.bytes_hint, "attention_split");
 }
 
 // ---------------------------------------------------------------------------------------------------------------

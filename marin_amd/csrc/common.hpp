@@ -129,15 +129,28 @@ struct marin_gpu {
     void download(void *dst, const void *src, size_t bytes);
     void *stage(const void *src, size_t bytes);  // copies into pinned memory; valid until the next stage()
 
-    // Launch accounting. With a profile attached, every launch records an event after itself, tagged with its kind
-    // and algorithmic bytes, so the gap between consecutive events is that kernel's time on the stream.
+    // Launch accounting. With a profile attached, every launch is tagged with its kind, algorithmic bytes and kernel
+    // name. The product and attention launchers then launch through hipExtLaunchKernelGGL with the two events of
+    // kernel_events(), which the runtime records at that kernel's own start and end; any other launch records one
+    // event after itself and runs from the previous event.
     enum Kind { OTHER = 0, GEMV = 1, ATTENTION = 2 };
     struct ProfileEntry {
+        hipEvent_t start;  // nullptr: from the previous entry's event
         hipEvent_t event;
         int kind;
         double bytes;
+        const char *name;
     };
     std::vector<ProfileEntry> *profile = nullptr;
     std::vector<hipEvent_t> event_pool;
-    void launched(int kind = OTHER, double bytes = 0.0);
+    size_t events_used = 0;
+    hipEvent_t pending_start = nullptr, pending_stop = nullptr;
+    // When set, product and attention launchers skip every kernel whose name differs (single-kernel timing graphs);
+    // a launcher that skipped sets `skipped` so no launch is counted.
+    const char *only = nullptr;
+    bool skipped = false;
+    hipEvent_t next_event();
+    // Two events for a kernel's own start and end when profiling (both nullptr otherwise); launched() takes them.
+    void kernel_events(hipEvent_t &start, hipEvent_t &stop);
+    void launched(int kind = OTHER, double bytes = 0.0, const char *name = nullptr);
 };

@@ -113,17 +113,32 @@ void marin_gpu::download(void *dst, const void *src, size_t bytes) {
     traffic.download_bytes += bytes;
 }
 
-void marin_gpu::launched(int kind, double bytes) {
-    traffic.launches++;
-    if (!profile) return;
-    const size_t i = profile->size();
-    if (i >= event_pool.size()) {
+hipEvent_t marin_gpu::next_event() {
+    if (events_used >= event_pool.size()) {
         hipEvent_t e;
         HIP_CHECK(hipEventCreate(&e));
         event_pool.push_back(e);
     }
-    HIP_CHECK(hipEventRecord(event_pool[i], stream));
-    profile->push_back({event_pool[i], kind, bytes});
+    return event_pool[events_used++];
+}
+
+void marin_gpu::kernel_events(hipEvent_t &start, hipEvent_t &stop) {
+    start = stop = nullptr;
+    if (!profile) return;
+    start = pending_start = next_event();
+    stop = pending_stop = next_event();
+}
+
+void marin_gpu::launched(int kind, double bytes, const char *name) {
+    traffic.launches++;
+    if (!profile) return;
+    hipEvent_t e = pending_stop;
+    if (!e) {
+        e = next_event();
+        HIP_CHECK(hipEventRecord(e, stream));
+    }
+    profile->push_back({pending_start, e, kind, bytes, name});
+    pending_start = pending_stop = nullptr;
 }
 
 void *marin_gpu::stage(const void *src, size_t bytes) {

@@ -17,7 +17,7 @@
 
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
+#include <cstring>
 
 #include "gemv.hpp"
 
@@ -457,15 +457,24 @@ void launch_gemv(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     if (!tokens) return;
     if (tokens > GEMV_TOKENS) unsupported("tokens per product", GEMV_TOKENS, tokens);
     if (!gemv_supported(w)) unsupported("matrix-core product layout (group and columns multiples of 64)", 64, w->group);
-    if (tokens == 1 && gemv_decode_supported(w) && !getenv("MARIN_OLD_DECODE")) launch_gemv_decode(g, w, in, out);
-    else if (w->bf16_scales) launch_st<uint16_t>(g, w, in, out, tokens);
-    else launch_st<float>(g, w, in, out, tokens);
+    const char *name = "gemv_q";
+    if (tokens == 1 && gemv_decode_supported(w)) {
+        name = launch_gemv_decode(g, w, in, out);
+    } else {
+        if (g->only && strcmp(g->only, name)) return;
+        if (w->bf16_scales) launch_st<uint16_t>(g, w, in, out, tokens);
+        else launch_st<float>(g, w, in, out, tokens);
+    }
+    if (g->skipped) {
+        g->skipped = false;
+        return;
+    }
     // algorithmic bytes: codes + scales once, activations and outputs once
     const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;
     const double outs = out.mode == OUT_SILU ? (double)w->rows / 2 : (double)w->rows;
     const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * w->groups() * (w->bf16_scales ? 2 : 4) +
                          (double)tokens * w->cols * act + (double)tokens * outs * res;
-    g->launched(marin_gpu::GEMV, bytes);
+    g->launched(marin_gpu::GEMV, bytes, name);
 }
 
 }  // namespace marin

@@ -37,7 +37,8 @@ struct GemvOut {
 bool gemv_supported(const marin_quant_matrix *w);
 // The one-token product (gemv_decode.hip): the matrix-core arithmetic on a latency-first schedule.
 bool gemv_decode_supported(const marin_quant_matrix *w);
-void launch_gemv_decode(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out);
+// Returns the launched instantiation's name.
+const char *launch_gemv_decode(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out);
 void launch_gemv(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
 
 }  // namespace marin

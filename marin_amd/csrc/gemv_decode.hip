@@ -13,9 +13,11 @@
 //  - the launch is persistent: blocks take tiles b, b + grid, ... with a grid sized to what stays resident.
 // The prologue (activation loads, RMSNorm statistic, limbs) runs while the first windows of codes are in flight.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <cmath>
+#include <string>
 
 #include "gemv.hpp"
 
@@ -359,7 +361,10 @@ static int slice_windows(int windows) {
 }
 
 template <int BITS, int WG, int SM, typename ST>
-static void launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+    // the instantiation's name as rocprof prints it, for the launch profile
+    static const std::string name = "gemv_decode<" + std::to_string(BITS) + ", " + std::to_string(WG) + ", " +
+                                    std::to_string(SM) + ", " + (sizeof(ST) == 4 ? "float" : "unsigned short") + ">";
     const int windows = (int)(w->cols / 64);
     const int groups = windows / WG;
     const int tiles = (int)(w->rows_padded / 16);
@@ -375,29 +380,35 @@ static void launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, const Gem
         resident = 1;
     const int cu = std::max(g->cu_count, 1);
     const int blocks = std::min(tiles, std::min(resident, DECODE_BLOCKS_PER_CU) * cu);
-    kern<<<dim3((unsigned)blocks), dim3(64 * DW), lds, g->stream>>>(w->codes, (const ST *)w->scales, in, out,
-                                                                    (int)w->rows, (int)w->cols, tiles);
+    if (g->only && name != g->only) {
+        g->skipped = true;
+        return name.c_str();
+    }
+    hipEvent_t t0, t1;
+    g->kernel_events(t0, t1);
+    if (t0)
+        hipExtLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * DW), (uint32_t)lds, g->stream, t0, t1, 0u, w->codes,
+                              (const ST *)w->scales, in, out, (int)w->rows, (int)w->cols, tiles);
+    else
+        kern<<<dim3((unsigned)blocks), dim3(64 * DW), lds, g->stream>>>(w->codes, (const ST *)w->scales, in, out,
+                                                                        (int)w->rows, (int)w->cols, tiles);
+    return name.c_str();
 }
 
 template <int BITS, int WG, typename ST>
-static void launch_decode_sm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+static const char *launch_decode_sm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
     switch (slice_windows((int)(w->cols / 64))) {
-        case 4: launch_decode_t<BITS, WG, (WG > 4 ? WG : 4), ST>(g, w, in, out); break;
-        case 8: launch_decode_t<BITS, WG, 8, ST>(g, w, in, out); break;
-        default: launch_decode_t<BITS, WG, 24, ST>(g, w, in, out); break;
+        case 4: return launch_decode_t<BITS, WG, 4, ST>(g, w, in, out);
+        case 8: return launch_decode_t<BITS, WG, 8, ST>(g, w, in, out);
+        default: return launch_decode_t<BITS, WG, 24, ST>(g, w, in, out);
     }
 }
 
 template <typename ST>
-static void launch_decode_st(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+static const char *launch_decode_st(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
     const bool wg2 = w->group == 128;
-    if (w->bits == 8) {
-        if (wg2) launch_decode_sm<8, 2, ST>(g, w, in, out);
-        else launch_decode_sm<8, 1, ST>(g, w, in, out);
-    } else {
-        if (wg2) launch_decode_sm<4, 2, ST>(g, w, in, out);
-        else launch_decode_sm<4, 1, ST>(g, w, in, out);
-    }
+    if (w->bits == 8) return wg2 ? launch_decode_sm<8, 2, ST>(g, w, in, out) : launch_decode_sm<8, 1, ST>(g, w, in, out);
+    return wg2 ? launch_decode_sm<4, 2, ST>(g, w, in, out) : launch_decode_sm<4, 1, ST>(g, w, in, out);
 }
 
 bool gemv_decode_supported(const marin_quant_matrix *w) {
@@ -410,9 +421,9 @@ extern "C" void marin_decode_trace_read(unsigned long long *host) {
 }
 #endif
 
-void launch_gemv_decode(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
-    if (w->bf16_scales) launch_decode_st<uint16_t>(g, w, in, out);
-    else launch_decode_st<float>(g, w, in, out);
+const char *launch_gemv_decode(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
+    if (w->bf16_scales) return launch_decode_st<uint16_t>(g, w, in, out);
+    return launch_decode_st<float>(g, w, in, out);
 }
 
 }  // namespace marin

@@ -15,8 +15,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <memory>
+#include <string>
 
 #include "attention.hpp"
 #include "ops.hpp"
@@ -514,59 +516,130 @@ marin_status marin_qwen3_decode(marin_qwen3 *m, marin_qwen3_cache *c, size_t ste
     return guard([&] { decode(m, c, steps, tokens_out); });
 }
 
+// Runs one decode step with an event after every launch (and before every product and attention launch) and
+// returns the launches in order; products and attention are timed by their own start and end events.
+static std::vector<marin_launch_record> profile_launches(marin_qwen3 *m, marin_qwen3_cache *c) {
+    marin_gpu *g = m->gpu;
+    const size_t len = c->kv->len;
+    if (len == 0) throw Error(MARIN_SHAPE, "decode needs a forward pass first", 1, 0);
+    if (len + 1 > c->kv->capacity) shape("kv positions", c->kv->capacity, len + 1);
+    c->kv->reserve(len + 1);
+    if (!c->tokens_out) {
+        c->tokens_out = (uint32_t *)g->alloc(4, false);
+        c->tokens_cap = 1;
+    }
+    const uint32_t init[3] = {(uint32_t)(len - 1), (uint32_t)len, 0u};
+    void *staged = g->stage(init, sizeof(init));
+    HIP_CHECK(hipMemcpyAsync(c->state, staged, sizeof(init), hipMemcpyHostToDevice, g->stream));
+    std::vector<marin_gpu::ProfileEntry> entries;
+    entries.reserve(1024);
+    g->events_used = 0;
+    hipEvent_t start = g->next_event();
+    HIP_CHECK(hipEventRecord(start, g->stream));
+    g->profile = &entries;
+    try {
+        decode_step(m, c, len + 1);
+    } catch (...) {
+        g->profile = nullptr;
+        g->pending_start = g->pending_stop = nullptr;
+        throw;
+    }
+    g->profile = nullptr;
+    HIP_CHECK(hipStreamSynchronize(g->stream));
+    std::vector<marin_launch_record> out;
+    out.reserve(entries.size());
+    hipEvent_t prev = start;
+    for (const auto &en : entries) {
+        float ms = 0.0f;
+        HIP_CHECK(hipEventElapsedTime(&ms, en.start ? en.start : prev, en.event));
+        marin_launch_record r{};
+        r.kind = (uint32_t)en.kind;
+        r.bytes = en.bytes;
+        r.seconds = ms * 1e-3;
+        snprintf(r.name, sizeof(r.name), "%s", en.name ? en.name : "");
+        out.push_back(r);
+        prev = en.event;
+    }
+    c->kv->len = len + 1;
+    return out;
+}
+
 marin_status marin_qwen3_profile_step(marin_qwen3 *m, marin_qwen3_cache *c, marin_step_profile *out) {
     return guard([&] {
-        marin_gpu *g = m->gpu;
-        const size_t len = c->kv->len;
-        if (len == 0) throw Error(MARIN_SHAPE, "decode needs a forward pass first", 1, 0);
-        if (len + 1 > c->kv->capacity) shape("kv positions", c->kv->capacity, len + 1);
-        c->kv->reserve(len + 1);
-        if (!c->tokens_out) {
-            c->tokens_out = (uint32_t *)g->alloc(4, false);
-            c->tokens_cap = 1;
-        }
-        const uint32_t init[3] = {(uint32_t)(len - 1), (uint32_t)len, 0u};
-        void *staged = g->stage(init, sizeof(init));
-        HIP_CHECK(hipMemcpyAsync(c->state, staged, sizeof(init), hipMemcpyHostToDevice, g->stream));
-        std::vector<marin_gpu::ProfileEntry> entries;
-        entries.reserve(1024);
-        hipEvent_t start;
-        HIP_CHECK(hipEventCreate(&start));
-        HIP_CHECK(hipEventRecord(start, g->stream));
-        g->profile = &entries;
-        try {
-            decode_step(m, c, len + 1);
-        } catch (...) {
-            g->profile = nullptr;
-            (void)hipEventDestroy(start);
-            throw;
-        }
-        g->profile = nullptr;
-        HIP_CHECK(hipStreamSynchronize(g->stream));
         marin_step_profile p{};
-        hipEvent_t prev = start;
-        for (auto &e : entries) {
-            float ms = 0.0f;
-            HIP_CHECK(hipEventElapsedTime(&ms, prev, e.event));
-            const double s = ms * 1e-3;
-            if (e.kind == marin_gpu::GEMV) {
-                p.gemv_seconds += s;
-                p.gemv_bytes += e.bytes;
+        for (const auto &r : profile_launches(m, c)) {
+            if (r.kind == marin_gpu::GEMV) {
+                p.gemv_seconds += r.seconds;
+                p.gemv_bytes += r.bytes;
                 p.gemv_launches++;
-            } else if (e.kind == marin_gpu::ATTENTION) {
-                p.attention_seconds += s;
-                p.attention_bytes += e.bytes;
+            } else if (r.kind == marin_gpu::ATTENTION) {
+                p.attention_seconds += r.seconds;
+                p.attention_bytes += r.bytes;
                 p.attention_launches++;
             } else {
-                p.other_seconds += s;
+                p.other_seconds += r.seconds;
                 p.other_launches++;
             }
-            p.step_seconds += s;
-            prev = e.event;
+            p.step_seconds += r.seconds;
         }
-        (void)hipEventDestroy(start);
-        c->kv->len = len + 1;
         *out = p;
+    });
+}
+
+marin_status marin_qwen3_time_kernel(marin_qwen3 *m, marin_qwen3_cache *c, const char *name, int reps,
+                                     double *seconds_per_launch, uint32_t *launches_per_pass) {
+    return guard([&] {
+        marin_gpu *g = m->gpu;
+        if (!name || !*name) shape("kernel name", 1, 0);
+        if (reps < 1) shape("timing repetitions", 1, (size_t)reps);
+        if (c->kv->len == 0) throw Error(MARIN_SHAPE, "timing needs a forward pass first", 1, 0);
+        const std::string only = name;
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        const uint64_t before = g->traffic.launches;
+        HIP_CHECK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
+        g->only = only.c_str();
+        try {
+            pass(m, c, 1, c->kv->capacity, 0);
+        } catch (...) {
+            g->only = nullptr;
+            g->skipped = false;
+            hipGraph_t junk = nullptr;
+            (void)hipStreamEndCapture(g->stream, &junk);
+            if (junk) (void)hipGraphDestroy(junk);
+            throw;
+        }
+        g->only = nullptr;
+        HIP_CHECK(hipStreamEndCapture(g->stream, &graph));
+        const uint64_t launches = g->traffic.launches - before;
+        if (launches == 0) {
+            (void)hipGraphDestroy(graph);
+            throw Error(MARIN_SHAPE, "no launch of that kernel in a decode pass", 1, 0);
+        }
+        hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        hip_check(e, "hipGraphInstantiate");
+        hipEvent_t a = g->next_event(), b = g->next_event();
+        float ms = 0.0f;
+        e = hipGraphLaunch(exec, g->stream);  // warm-up
+        if (e == hipSuccess) e = hipEventRecord(a, g->stream);
+        for (int r = 0; r < reps && e == hipSuccess; ++r) e = hipGraphLaunch(exec, g->stream);
+        if (e == hipSuccess) e = hipEventRecord(b, g->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        (void)hipGraphExecDestroy(exec);
+        hip_check(e, "timed kernel graph");
+        *seconds_per_launch = ms * 1e-3 / ((double)reps * (double)launches);
+        *launches_per_pass = (uint32_t)launches;
+    });
+}
+
+marin_status marin_qwen3_profile_launches(marin_qwen3 *m, marin_qwen3_cache *c, marin_launch_record *out,
+                                          size_t cap, size_t *count) {
+    return guard([&] {
+        const auto recs = profile_launches(m, c);
+        for (size_t i = 0; i < recs.size() && i < cap; ++i) out[i] = recs[i];
+        *count = recs.size();
     });
 }
 

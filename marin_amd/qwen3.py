@@ -11,7 +11,7 @@ import ctypes as C
 import numpy as np
 
 from . import Gpu, KvFormat, check
-from ._lib import Qwen3ConfigC, StepProfileC, alive, lib
+from ._lib import LaunchRecordC, Qwen3ConfigC, StepProfileC, alive, lib
 
 # Benchmark shapes (BASELINE.json configs 0 and 3).
 SHAPES = {
@@ -120,6 +120,22 @@ class Qwen3:
         p = StepProfileC()
         check(lib.marin_qwen3_profile_step(self._h, cache._h, C.byref(p)))
         return {f: getattr(p, f) for f, _ in StepProfileC._fields_}
+
+    def profile_launches(self, cache: "Qwen3Cache") -> list:
+        """One decode step with events around every launch: [(kind, kernel name, algorithmic bytes, seconds)] in
+        launch order (kind 0 other, 1 quantized product, 2 attention)."""
+        cap = 4096
+        recs = (LaunchRecordC * cap)()
+        n = C.c_size_t()
+        check(lib.marin_qwen3_profile_launches(self._h, cache._h, recs, cap, C.byref(n)))
+        return [(int(r.kind), r.name.decode(), float(r.bytes), float(r.seconds)) for r in recs[:min(n.value, cap)]]
+
+    def time_kernel(self, cache: "Qwen3Cache", name: str, reps: int = 20) -> tuple:
+        """Mean seconds per launch of kernel `name` over graph replays of one decode pass's launches of it, and the
+        launches per pass (the cache's activations are left unspecified)."""
+        sec, n = C.c_double(), C.c_uint32()
+        check(lib.marin_qwen3_time_kernel(self._h, cache._h, name.encode(), reps, C.byref(sec), C.byref(n)))
+        return sec.value, n.value
 
     def __del__(self):
         if getattr(self, "_h", None) and alive():
