@@ -119,35 +119,58 @@ __device__ __forceinline__ void store_kv(uint8_t *row, int e, float x) {
     }
 }
 
-// RMSNorm(weight) then RoPE at `pos` of one head, by one wave: lane i takes the pairs (i, i + hd/2), i < hd/2 (hd even,
-// at most 256). Norm: x * (1 / sqrtf(mean(x^2) + eps)) * w (kernels.cu:51-60); RoPE: angle = pos * freq[i] with the
-// host's powf table, sincosf on the device, (a, b) -> (a cos - b sin, b cos + a sin) (ops.rs:56-95).
-__device__ __forceinline__ void norm_rope_head(const float *__restrict__ src, const float *__restrict__ w,
-                                               const float *__restrict__ freq, uint32_t pos, int hd, float eps,
-                                               int lane, float a[2], float b[2]) {
+// One head's RMSNorm(weight) + RoPE inputs held by one wave: lane i takes the pairs (i, i + hd/2), i < hd/2 (hd
+// even, at most 256), with their norm weights and RoPE frequencies.
+struct HeadIn {
+    float a[2], b[2], wa[2], wb[2], f[2];
+};
+
+__device__ __forceinline__ HeadIn load_head(const float *__restrict__ src, const float *__restrict__ w,
+                                            const float *__restrict__ freq, int hd, int lane) {
     const int half = hd / 2;
+    HeadIn h;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = lane + 64 * k;
-        a[k] = i < half ? src[i] : 0.0f;
-        b[k] = i < half ? src[i + half] : 0.0f;
+        const bool in = i < half;
+        h.a[k] = in ? src[i] : 0.0f;
+        h.b[k] = in ? src[i + half] : 0.0f;
+        h.wa[k] = in ? w[i] : 0.0f;
+        h.wb[k] = in ? w[i + half] : 0.0f;
+        h.f[k] = in ? freq[i] : 0.0f;
     }
+    return h;
+}
+
+// Norm: x * (1 / sqrtf(mean(x^2) + eps)) * w (kernels.cu:51-60); RoPE: angle = pos * freq[i] with the host's powf
+// table, sincosf on the device, (a, b) -> (a cos - b sin, b cos + a sin) (ops.rs:56-95).
+__device__ __forceinline__ void finish_head(const HeadIn &h, uint32_t pos, int hd, float eps, int lane, float a[2],
+                                            float b[2]) {
+    const int half = hd / 2;
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) s += a[k] * a[k] + b[k] * b[k];
+    for (int k = 0; k < 2; ++k) s += h.a[k] * h.a[k] + h.b[k] * h.b[k];
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
     const float scale = 1.0f / sqrtf(s / (float)hd + eps);
     const float position = (float)pos;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = lane + 64 * k;
+        a[k] = b[k] = 0.0f;
         if (i >= half) continue;
-        const float x = a[k] * scale * w[i], y = b[k] * scale * w[i + half];
+        const float x = h.a[k] * scale * h.wa[k], y = h.b[k] * scale * h.wb[k];
         float sn, cs;
-        sincosf(position * freq[i], &sn, &cs);
+        sincosf(position * h.f[k], &sn, &cs);
         a[k] = x * cs - y * sn;
         b[k] = y * cs + x * sn;
     }
+}
+
+// RMSNorm(weight) then RoPE at `pos` of one head, by one wave.
+__device__ __forceinline__ void norm_rope_head(const float *__restrict__ src, const float *__restrict__ w,
+                                               const float *__restrict__ freq, uint32_t pos, int hd, float eps,
+                                               int lane, float a[2], float b[2]) {
+    finish_head(load_head(src, w, freq, hd, lane), pos, hd, eps, lane, a, b);
 }
 
 #ifdef ATTN_TIMING
@@ -540,6 +563,442 @@ __global__ __launch_bounds__(64 * NW) void attention_split(
     for (int o = threadIdx.x; o < nrows * hd; o += NT) write_out(o / hd, o % hd, q_s[o / hd][o % hd] / ml_s[o / hd][1]);
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// One-token decode attention (every sequence adds one position), built for latency.
+//
+// grid: x = chunk of the context, y = kv head, z = sequence; 4 waves. A workgroup takes `chunk` positions of one kv
+// head for all `group` query heads of it (R >= group rows). Lanes work in groups of LPP per position with 8 head
+// values a lane, so a wave covers 64 / LPP positions per step; the workgroup's steps are issued as one burst of loads
+// (up to U per lane for keys and as many for values) right after its page addresses are known, so a chunk costs one
+// memory round trip. With FUSE, q and the new key get RMSNorm + RoPE in the kernel; the workgroup whose chunk holds
+// the new position takes that key and value from LDS (rounded to the cache format, exactly as stored) and stores them
+// into the cache without waiting for the store. Chunks write a record (max, sum, weighted values) per row with
+// agent-coherent stores; the last chunk of a (sequence, kv head) to arrive merges all of them in chunk order.
+
+// Eight values of a new key or value row in the cache's storage format (store_kv's rounding).
+template <int F>
+__device__ __forceinline__ Raw8<F> to_raw(const float *v) {
+    Raw8<F> r;
+    if constexpr (F == MARIN_KV_F32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.w[i / 4][i % 4] = __float_as_uint(v[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            uint32_t lo, hi;
+            if constexpr (F == MARIN_KV_F16) {
+                const float a = v[i] != v[i] ? v[i] : fminf(fmaxf(v[i], -65504.0f), 65504.0f);
+                const float b = v[i + 1] != v[i + 1] ? v[i + 1] : fminf(fmaxf(v[i + 1], -65504.0f), 65504.0f);
+                lo = __builtin_bit_cast(uint16_t, (_Float16)a);
+                hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+            } else {
+                auto rne = [](float x) {
+                    const unsigned u = __float_as_uint(x);
+                    return (u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+                };
+                lo = rne(v[i]);
+                hi = rne(v[i + 1]);
+            }
+            r.w[0][i / 2] = (lo & 0xffffu) | (hi << 16);
+        }
+    }
+    return r;
+}
+
+constexpr int DEC_NW = 4;        // waves per workgroup
+constexpr int DEC_MAX_SPLITS = 64;  // chunks merged by the last workgroup
+
+// Steps of key/value loads in flight per lane: one workgroup per compute unit leaves the registers for deeper bursts
+// when the group (rows) is small.
+template <int F, int R>
+__host__ __device__ constexpr int dec_umax() { return F == MARIN_KV_F32 ? (R <= 4 ? 6 : 4) : (R <= 4 ? 12 : 8); }
+
+template <int F, int LPP, bool BF16IO, int R, bool FUSE>
+__global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
+    const void *__restrict__ qv, AttnFuse fuse, const uint64_t *__restrict__ tables, size_t table_stride,
+    const uint32_t *__restrict__ ctx_lens, KvGeom geom, int heads, int kv_heads, int chunk, int splits, float scale,
+    float *__restrict__ part, int part_bytes, uint32_t *__restrict__ counters, void *__restrict__ out) {
+    constexpr int NW = DEC_NW, NT = 64 * NW;
+    constexpr int HMAX = 8 * LPP;          // head values covered by the lanes of one position
+    constexpr int PPW = 64 / LPP;          // positions per wave step
+    constexpr int STEP = NW * PPW;         // positions per workgroup step
+    constexpr int U = dec_umax<F, R>();
+    constexpr int MAXPG = U * STEP + 1;    // page addresses of one chunk (pages of at least one position)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int slot = lane / LPP, sub = lane % LPP;
+    const int hd = (int)geom.head_dim;
+    const int group = heads / kv_heads;
+    const int kvh = blockIdx.y, b = blockIdx.z, split = blockIdx.x;
+    const int ctx = (int)ctx_lens[b];
+    const int first = split * chunk;
+    if (first >= ctx) return;
+    const int count = min(chunk, ctx - first);
+    const int used = (ctx + chunk - 1) / chunk;
+    const int d = sub * 8;
+    const int dl = min(d, hd - 8);  // load offset: lanes past the head's end read its last 8 values, weighted by 0
+    const size_t es = F == MARIN_KV_F32 ? 4 : 2;
+    const uint64_t head_off = (uint64_t)kvh * geom.head_bytes + geom.layer_offset;
+    const uint32_t pmask = (1u << geom.page_shift) - 1u;
+    const uint64_t *table = tables + (size_t)b * table_stride;
+    const int newpos = ctx - 1;
+    const bool owns_new = FUSE && newpos >= first && newpos < first + count;
+    ATT_T(0);
+
+    __shared__ uint64_t pages_s[MAXPG];
+    __shared__ float q_s[R][HMAX];
+    __shared__ float new_s[2][HMAX];  // the new key (normalized and rotated) and value
+    __shared__ float red_acc[NW * PPW][R][HMAX];
+    __shared__ float red_ml[NW * PPW][R][2];
+    __shared__ float ml_s[R][2];
+
+    // ---- one burst: the query inputs (with FUSE, the raw q heads of this kv head and, in the workgroup that owns the
+    // new position, the raw new key and value), issued first so they are not queued behind other workgroups' rows,
+    // then the page addresses
+    constexpr int QPW = (R + NW - 1) / NW;  // q heads per wave
+    HeadIn qin[QPW], kin;
+    float vin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (FUSE) {
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int r = wave + j * NW;
+            if (r < group) qin[j] = load_head(fuse.qkv + (size_t)(kvh * group + r) * hd, fuse.q_norm, fuse.freq, hd, lane);
+        }
+        if (owns_new && wave == NW - 1) {
+            kin = load_head(fuse.qkv + (size_t)(heads + kvh) * hd, fuse.k_norm, fuse.freq, hd, lane);
+            const float *vsrc = fuse.qkv + (size_t)(heads + kv_heads + kvh) * hd;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) vin[k] = lane + 64 * k < hd ? vsrc[lane + 64 * k] : 0.0f;
+        }
+    } else {
+        for (int i = threadIdx.x; i < group * hd; i += NT) {
+            const int r = i / hd, e = i % hd;
+            const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
+            if constexpr (BF16IO) q_s[r][e] = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(qv)[at]);
+            else q_s[r][e] = reinterpret_cast<const float *>(qv)[at];
+        }
+    }
+    const int page0 = first >> geom.page_shift;
+    const int npages = ((first + count - 1) >> geom.page_shift) - page0 + 1;
+    for (int i = threadIdx.x; i < npages; i += NT) pages_s[i] = table[page0 + i] + head_off;
+    __syncthreads();
+    ATT_T(1);
+
+    // ---- every key and value row of the chunk in flight at once (clamped positions past the chunk's end)
+    auto row_ptr = [&](int which, int p) {
+        const uint32_t pos = (uint32_t)(first + p);
+        return reinterpret_cast<const uint8_t *>(pages_s[(pos >> geom.page_shift) - page0] +
+                                                 (which ? geom.value_offset : 0) + (uint64_t)(pos & pmask) * hd * es);
+    };
+    const int steps = (count + STEP - 1) / STEP;  // <= U
+    // Every step's rows are loaded unconditionally (positions past the chunk clamped to its last one): a load under
+    // a branch would make the wait for the query inputs below also wait for every row. Rows of positions past the
+    // chunk are zeroed when used, so their weight 0 never meets a non-finite value.
+    Raw8<F> kr[U], vr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int p = min(wave * PPW + slot + u * STEP, count - 1);
+        load_raw<F, true>(row_ptr(0, p), dl, hd, kr[u]);
+        load_raw<F, true>(row_ptr(1, p), dl, hd, vr[u]);
+    }
+    // ---- with FUSE: q and the new key normalized and rotated while the rows are in flight
+    if constexpr (FUSE) {
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int r = wave + j * NW;
+            if (r < group) {
+                float a2[2], b2[2];
+                finish_head(qin[j], (uint32_t)newpos, hd, fuse.eps, lane, a2, b2);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int i = lane + 64 * k;
+                    if (i < hd / 2) {
+                        q_s[r][i] = a2[k];
+                        q_s[r][i + hd / 2] = b2[k];
+                    }
+                }
+            }
+        }
+        if (owns_new && wave == NW - 1) {
+            float a2[2], b2[2];
+            finish_head(kin, (uint32_t)newpos, hd, fuse.eps, lane, a2, b2);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int i = lane + 64 * k;
+                if (i < hd / 2) {
+                    new_s[0][i] = a2[k];
+                    new_s[0][i + hd / 2] = b2[k];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (lane + 64 * k < hd) new_s[1][lane + 64 * k] = vin[k];
+        }
+        __syncthreads();
+    }
+    ATT_T(2);
+    float q[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[r][i] = (r < group && d + i < hd) ? q_s[r][d + i] : 0.0f;
+
+    // ---- scores, then one softmax pass over this lane group's positions
+    float sc[R][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int p = wave * PPW + slot + u * STEP;
+        if (owns_new && first + p == newpos) {
+            float kn[8], vn[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kn[i] = d + i < hd ? new_s[0][d + i] : 0.0f;
+                vn[i] = d + i < hd ? new_s[1][d + i] : 0.0f;
+            }
+            kr[u] = to_raw<F>(kn);
+            vr[u] = to_raw<F>(vn);
+        }
+        const bool valid = u < steps && p < count;
+        if (!valid) {
+#pragma unroll
+            for (int j = 0; j < (F == MARIN_KV_F32 ? 2 : 1); ++j) kr[u].w[j] = vr[u].w[j] = (u32x4){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dot += q[r][i] * elem<F>(kr[u], i);
+            dot = group_sum<LPP>(dot);
+            sc[r][u] = valid ? dot * scale : -INFINITY;
+        }
+    }
+    float mrow[R], lrow[R], acc[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; ++u) mx = fmaxf(mx, sc[r][u]);
+        mrow[r] = mx;
+        lrow[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[r][i] = 0.0f;
+        if (mx != -INFINITY) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float e = sc[r][u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r][u] - mx);
+                lrow[r] += e;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[r][i] += e * elem<F>(vr[u], i);
+            }
+        }
+    }
+    // ---- every (wave, position slot) leaves its maximum, sum and weighted values in LDS; the workgroup combines
+    // the NS = NW * PPW partials in a fixed order
+    ATT_T(3);
+    constexpr int NS = NW * PPW;
+    const int ps = wave * PPW + slot;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (d + i < hd) red_acc[ps][r][d + i] = acc[r][i];
+        if (sub == 0) {
+            red_ml[ps][r][0] = mrow[r];
+            red_ml[ps][r][1] = lrow[r];
+        }
+    }
+    __syncthreads();
+    // the partials' weights: a thread per (row, partial), the row's maximum over its partials by lane shuffles
+    // (NS consecutive lanes, NS a power of two <= 64)
+    {
+        const int r = threadIdx.x / NS, w = threadIdx.x % NS;
+        const bool on = r < group;
+        const float mw = on ? red_ml[w][r][0] : -INFINITY;
+        float mn = mw;
+#pragma unroll
+        for (int o = 1; o < NS; o <<= 1) mn = fmaxf(mn, __shfl_xor(mn, o));
+        const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mn);
+        float l = on ? red_ml[w][r][1] * wt : 0.0f;
+#pragma unroll
+        for (int o = 1; o < NS; o <<= 1) l += __shfl_xor(l, o);
+        __syncthreads();  // every thread has read red_ml before it is overwritten with weights
+        if (on) red_ml[w][r][0] = wt;
+        if (on && w == 0) {
+            ml_s[r][0] = mn;
+            ml_s[r][1] = l;
+        }
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < group * hd; o += NT) {
+        const int r = o / hd, e = o % hd;
+        float a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NS; ++w) a += red_acc[w][r][e] * red_ml[w][r][0];
+        q_s[r][e] = a;  // the workgroup's weighted values (q is in registers)
+    }
+    __syncthreads();
+
+    auto write_out = [&](int r, int e, float v) {
+        const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
+        if constexpr (BF16IO) {
+            const unsigned u = __float_as_uint(v);
+            reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        } else {
+            reinterpret_cast<float *>(out)[at] = v;
+        }
+    };
+    // the new key and value, stored for later steps (this launch read them from LDS); stored last, as a store under
+    // a branch earlier on would make the waits for the rows drain every load in flight
+    if (owns_new && wave == NW - 1) {
+        const uint64_t page = table[newpos >> geom.page_shift] + head_off + (uint64_t)(newpos & pmask) * hd * es;
+        for (int i = lane; i < hd; i += 64) {
+            store_kv<F>(reinterpret_cast<uint8_t *>(page), i, new_s[0][i]);
+            store_kv<F>(reinterpret_cast<uint8_t *>(page + geom.value_offset), i, new_s[1][i]);
+        }
+    }
+    if (used == 1) {
+        for (int o = threadIdx.x; o < group * hd; o += NT) write_out(o / hd, o % hd, q_s[o / hd][o % hd] / ml_s[o / hd][1]);
+        return;
+    }
+
+    // ---- record of this chunk (max, sum, weighted values per row); attention_decode_merge combines them
+    const int RS = rec_floats(hd);
+    float *rec = part + (((size_t)b * heads + kvh * group) * splits + split) * (size_t)RS;
+    for (int o = threadIdx.x; o < group * (RS / 4); o += NT) {
+        const int r = o / (RS / 4), c4 = o % (RS / 4);
+        float4 v;
+        if (c4 == 0) {
+            v = make_float4(ml_s[r][0], ml_s[r][1], 0.0f, 0.0f);
+        } else {
+            const int e = 4 * (c4 - 1);
+            v = make_float4(e < hd ? q_s[r][e] : 0.0f, e + 1 < hd ? q_s[r][e + 1] : 0.0f,
+                            e + 2 < hd ? q_s[r][e + 2] : 0.0f, e + 3 < hd ? q_s[r][e + 3] : 0.0f);
+        }
+        *reinterpret_cast<float4 *>(rec + (size_t)r * splits * RS + 4 * c4) = v;
+    }
+    ATT_T(6);
+}
+
+// The chunks of one (sequence, kv head) combined with log-sum-exp weights, in chunk order: a workgroup per
+// (kv head, sequence). Chunk weights are computed a lane per (row, chunk) with the row's chunks in consecutive lanes
+// (a power-of-two span P, so the row's maximum and sum are lane shuffles); the weighted values are summed a thread
+// per (row, 4 values, half of the chunks), every record word of the thread loaded in one burst.
+template <bool BF16IO, int R>
+__global__ __launch_bounds__(256) void attention_decode_merge(const float *__restrict__ part,
+                                                              const uint32_t *__restrict__ ctx_lens, int hd,
+                                                              int heads, int kv_heads, int chunk, int splits,
+                                                              void *__restrict__ out) {
+    constexpr int NT = 256;
+    __shared__ float wt_s[R][DEC_MAX_SPLITS];
+    __shared__ float l_s[R];
+    __shared__ float half_s[R][256];
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const int group = heads / kv_heads;
+    const int ctx = (int)ctx_lens[b];
+    const int used = (ctx + chunk - 1) / chunk;
+    if (used <= 1) return;  // a context of one chunk was written by attention_decode itself
+    const int RS = rec_floats(hd);
+    const float *rec0 = part + ((size_t)b * heads + kvh * group) * splits * (size_t)RS;
+    auto write_out = [&](int r, int e, float v) {
+        const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
+        if constexpr (BF16IO) {
+            const unsigned u = __float_as_uint(v);
+            reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        } else {
+            reinterpret_cast<float *>(out)[at] = v;
+        }
+    };
+    // chunk headers: lane per (row, chunk) over a span P (power of two >= used, <= 64)
+    int P = 1;
+    while (P < used) P <<= 1;
+    float2 hdr[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = threadIdx.x + h * NT, r = i / P, k = i % P;
+        hdr[h] = (r < group && k < used) ? *reinterpret_cast<const float2 *>(rec0 + ((size_t)r * splits + k) * RS)
+                                         : make_float2(-INFINITY, 0.0f);
+    }
+    // weighted values: a thread per (row, 4 values, share of the chunks): chunk k of share h is h + halves * j; one
+    // unrolled burst of clamped loads per pass of J chunks, the first issued before the weights are known
+    constexpr int J = 16;
+    const int c4n = (hd + 3) / 4;
+    const int pairs = group * c4n;
+    const int halves = pairs * 2 <= NT ? 2 : 1;
+    const int per = (used + halves - 1) / halves;
+    const int passes = (per + J - 1) / J;
+    float4 v[J];
+    auto burst = [&](int col, int hf, int pass) {
+        const int r = col / c4n, e4 = col - r * c4n;
+        const float *base = rec0 + (size_t)r * splits * RS + 4 + 4 * e4;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int k = min(hf + halves * (pass * J + j), used - 1);
+            v[j] = *reinterpret_cast<const float4 *>(base + (size_t)k * RS);
+        }
+    };
+    auto accumulate = [&](int col, int hf, int pass, float a[4]) {
+        const int r = col / c4n;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int k = hf + halves * (pass * J + j);
+            const float w = k < used ? wt_s[r][k] : 0.0f;
+            a[0] += v[j].x * w;
+            a[1] += v[j].y * w;
+            a[2] += v[j].z * w;
+            a[3] += v[j].w * w;
+        }
+    };
+    const int hf0 = (int)threadIdx.x / pairs;
+    const int col0 = (int)threadIdx.x - hf0 * pairs;
+    const bool active = hf0 < halves;  // threads of the first column sweep
+    if (active) burst(col0, hf0, 0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = threadIdx.x + h * NT, rr = i / P, k = i % P;
+        float m = hdr[h].x;
+        for (int o = 1; o < P; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float w = hdr[h].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(hdr[h].x - m);
+        float l = hdr[h].y * w;
+        for (int o = 1; o < P; o <<= 1) l += __shfl_xor(l, o);
+        if (rr < group && k < used) wt_s[rr][k] = w;
+        if (rr < group && k == 0) l_s[rr] = l;
+    }
+    __syncthreads();
+    if (halves == 2) {
+        // pairs <= NT / 2: every column has both shares; the second share's sums meet the first's in LDS
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int r = col0 / c4n, e4 = col0 - r * c4n;
+        if (active) {
+            for (int pass = 0; pass < passes; ++pass) {
+                if (pass) burst(col0, hf0, pass);
+                accumulate(col0, hf0, pass, a);
+            }
+            if (hf0 == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) half_s[r][(4 * e4 + j) & 255] = a[j];
+            }
+        }
+        __syncthreads();
+        if (active && hf0 == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * e4 + j < hd) write_out(r, 4 * e4 + j, (a[j] + half_s[r][4 * e4 + j]) / l_s[r]);
+        }
+    } else {
+        // one share: a thread per column, several columns a thread when there are more than NT
+        for (int col = (int)threadIdx.x; col < pairs; col += NT) {
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int pass = 0; pass < passes; ++pass) {
+                if (pass || col != col0) burst(col, 0, pass);
+                accumulate(col, 0, pass, a);
+            }
+            const int r = col / c4n, e4 = col - r * c4n;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * e4 + j < hd) write_out(r, 4 * e4 + j, a[j] / l_s[r]);
+        }
+    }
+}
+
 #ifndef ATTN_NW
 #define ATTN_NW 4
 #endif
@@ -629,6 +1088,74 @@ static void launch_split_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int 
     }
 }
 
+#ifndef ATTN_DEC_BPC
+#define ATTN_DEC_BPC 1
+#endif
+
+template <int F, int LPP, bool BF16IO, int R, bool FUSE>
+static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    hipEvent_t t0, t1;
+    g->kernel_events(t0, t1);
+    auto kern = attention_decode<F, LPP, BF16IO, R, FUSE>;
+    if (t0)
+        hipExtLaunchKernelGGL(kern, grid, dim3(64 * DEC_NW), 0u, g->stream, t0, t1, 0u, a.q, a.fuse, a.tables,
+                              a.table_stride, a.ctx, a.geom, (int)a.heads, (int)a.kv_heads, chunk, splits, scale,
+                              a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+    else
+        kern<<<grid, dim3(64 * DEC_NW), 0, g->stream>>>(a.q, a.fuse, a.tables, a.table_stride, a.ctx, a.geom,
+                                                        (int)a.heads, (int)a.kv_heads, chunk, splits, scale,
+                                                        a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+}
+
+template <int F, int LPP, int R>
+static void launch_decode_io(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    if (a.fuse.qkv) launch_decode<F, LPP, false, R, true>(g, a, grid, chunk, splits, scale);
+    else if (a.bf16_io) launch_decode<F, LPP, true, R, false>(g, a, grid, chunk, splits, scale);
+    else launch_decode<F, LPP, false, R, false>(g, a, grid, chunk, splits, scale);
+}
+
+template <int F>
+static void launch_decode_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    const bool r4 = a.heads / a.kv_heads <= 4;
+    switch (lanes_for(a.geom.head_dim)) {
+        case 4: r4 ? launch_decode_io<F, 4, 4>(g, a, grid, chunk, splits, scale)
+                   : launch_decode_io<F, 4, 8>(g, a, grid, chunk, splits, scale); break;
+        case 8: r4 ? launch_decode_io<F, 8, 4>(g, a, grid, chunk, splits, scale)
+                   : launch_decode_io<F, 8, 8>(g, a, grid, chunk, splits, scale); break;
+        case 16: r4 ? launch_decode_io<F, 16, 4>(g, a, grid, chunk, splits, scale)
+                    : launch_decode_io<F, 16, 8>(g, a, grid, chunk, splits, scale); break;
+        default: r4 ? launch_decode_io<F, 32, 4>(g, a, grid, chunk, splits, scale)
+                    : launch_decode_io<F, 32, 8>(g, a, grid, chunk, splits, scale); break;
+    }
+}
+
+// The one-token kernel's chunking for a context bound: about ATTN_DEC_BPC workgroups per compute unit, chunks a
+// multiple of one workgroup step and at most what one burst of loads covers; 0 when that needs more chunks than one
+// merge takes.
+static int decode_chunk(const AttentionArgs &a, int cu_count, int &splits) {
+    const int hd = (int)a.geom.head_dim;
+    const int step = DEC_NW * (64 / lanes_for((size_t)hd));
+    const bool r4 = a.heads / a.kv_heads <= 4;
+    const int umax = a.geom.format == MARIN_KV_F32 ? (r4 ? dec_umax<MARIN_KV_F32, 4>() : dec_umax<MARIN_KV_F32, 8>())
+                                                   : (r4 ? dec_umax<MARIN_KV_F16, 4>() : dec_umax<MARIN_KV_F16, 8>());
+    const size_t units = std::max<size_t>(a.kv_heads * a.batch, 1);
+    const size_t target = std::max<size_t>(1, ((size_t)ATTN_DEC_BPC * std::max(cu_count, 1) + units - 1) / units);
+    size_t chunk = (a.max_ctx + target - 1) / target;
+    chunk = (chunk + step - 1) / step * step;
+    chunk = std::min<size_t>(std::max<size_t>(chunk, (size_t)step), (size_t)umax * step);
+    const size_t n = (a.max_ctx + chunk - 1) / chunk;
+    if (n > (size_t)DEC_MAX_SPLITS) return 0;
+    splits = (int)std::max<size_t>(n, 1);
+    return (int)chunk;
+}
+
+static bool decode_kernel_fits(const AttentionArgs &a) {
+    const size_t hd = a.geom.head_dim, group = a.heads / a.kv_heads;
+    // the (row, partial) pairs of the workgroup's reduction take a thread each
+    const size_t partials = (size_t)DEC_NW * (64 / lanes_for(hd));
+    return a.tokens == 1 && hd % 8 == 0 && hd >= 8 && group <= 8 && partials * group <= 64 * DEC_NW;
+}
+
 void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     const size_t group = a.heads / a.kv_heads;
     const size_t rpb = (size_t)rows_per_block(a);
@@ -647,6 +1174,36 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     if (counters > a.counter_count) shape("attention chunk counters", counters, a.counter_count);
     // scores in the log2 domain: dot * (1/sqrt(hd)) * log2(e), weights 2^(s - max) with the hardware exp2
     const float scale = (float)(1.4426950408889634 / std::sqrt((double)a.geom.head_dim));
+    int dsplits = 0;
+    const int dchunk = decode_kernel_fits(a) ? decode_chunk(a, g->cu_count, dsplits) : 0;
+    if (dchunk) {
+        if (a.batch * a.kv_heads > a.counter_count) shape("attention chunk counters", a.batch * a.kv_heads, a.counter_count);
+        const size_t dneed = a.batch * a.heads * (size_t)dsplits * (size_t)rec_floats((int)a.geom.head_dim);
+        if (dsplits > 1 && dneed > a.partial_floats) shape("attention partial records (floats)", dneed, a.partial_floats);
+        if (a.partial_floats * 4 >= ((size_t)1 << 31))
+            unsupported("attention partial bytes", (size_t)1 << 31, a.partial_floats * 4);
+        if (g->only && strcmp(g->only, "attention_decode")) return;
+        dim3 dgrid((unsigned)dsplits, (unsigned)a.kv_heads, (unsigned)a.batch);
+        switch (a.geom.format) {
+            case MARIN_KV_F32: launch_decode_f<MARIN_KV_F32>(g, a, dgrid, dchunk, dsplits, scale); break;
+            case MARIN_KV_F16: launch_decode_f<MARIN_KV_F16>(g, a, dgrid, dchunk, dsplits, scale); break;
+            default: launch_decode_f<MARIN_KV_BF16>(g, a, dgrid, dchunk, dsplits, scale); break;
+        }
+        g->launched(marin_gpu::ATTENTION, a.bytes_hint, "attention_decode");
+        if (dsplits > 1 && !(g->only && strcmp(g->only, "attention_decode_merge"))) {
+            dim3 mgrid((unsigned)a.kv_heads, (unsigned)a.batch);
+            const bool r4 = a.heads / a.kv_heads <= 4;
+            if (a.bf16_io) {
+                if (r4) attention_decode_merge<true, 4><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
+                else attention_decode_merge<true, 8><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
+            } else {
+                if (r4) attention_decode_merge<false, 4><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
+                else attention_decode_merge<false, 8><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
+            }
+            g->launched(marin_gpu::OTHER, 0.0, "attention_decode_merge");
+        }
+        return;
+    }
     if (g->only && strcmp(g->only, "attention_split")) return;
     dim3 grid((unsigned)splits, (unsigned)(a.kv_heads * row_groups), (unsigned)a.batch);
     switch (a.geom.format) {
@@ -697,7 +1254,10 @@ KvGeom marin_kv::geom(size_t layer) const {
     g.head_dim = (uint32_t)head_dim;
     g.head_bytes = (uint64_t)MARIN_PAGE_TOKENS * head_dim * kv_elem_bytes(format);
     g.value_offset = g.head_bytes * kv_heads;
-    g.layer_offset = (uint64_t)layer * 2 * g.value_offset;
+    // A slab is [layer][page][K, V][kv head][position][head value]: one layer's pages of a slab are one contiguous
+    // run, so a layer's context spans few address-translation regions. A page pointer is its slab plus the page's
+    // slot times one page-layer block, and every layer adds its own offset.
+    g.layer_offset = (uint64_t)layer * MARIN_SLAB_PAGES * 2 * g.value_offset;
     g.format = (uint32_t)format;
     return g;
 }
@@ -726,7 +1286,7 @@ void marin_kv::reserve(size_t positions) {
                     throw k;
                 }
             }
-            host_ptrs[i] = (uint64_t)(uintptr_t)slabs[slab] + (uint64_t)slot * page_bytes();
+            host_ptrs[i] = (uint64_t)(uintptr_t)slabs[slab] + (uint64_t)slot * (page_bytes() / layers);
         }
         if (table.ids.size() > first_new) {
             const size_t n = table.ids.size() - first_new;
