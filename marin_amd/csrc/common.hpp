@@ -128,6 +128,11 @@ struct marin_gpu {
     void upload(void *dst, const void *src, size_t bytes);  // synchronous with respect to the host data
     void download(void *dst, const void *src, size_t bytes);
     void *stage(const void *src, size_t bytes);  // copies into pinned memory; valid until the next stage()
+    // Grow-only device scratch for multi-token products (activation limbs); waits for the stream before it grows.
+    // Never reached by a one-token decode step.
+    void *work = nullptr;
+    size_t work_bytes = 0;
+    void *workspace(size_t bytes);
 
     // Launch accounting. With a profile attached, every launch is tagged with its kind, algorithmic bytes and kernel
     // name. The product and attention launchers then launch through hipExtLaunchKernelGGL with the two events of

@@ -88,8 +88,22 @@ void marin_gpu::release(void *p) {
     if (closing && live == 0) destroy();
 }
 
+void *marin_gpu::workspace(size_t bytes) {
+    if (bytes <= work_bytes) return work;
+    HIP_CHECK(hipStreamSynchronize(stream));
+    if (work) (void)hipFree(work);
+    work = nullptr;
+    work_bytes = 0;
+    const size_t want = std::max<size_t>(bytes, (size_t)1 << 22);
+    hip_check(hipMalloc(&work, want), "hipMalloc (workspace)");
+    work_bytes = want;
+    traffic.allocations++;
+    return work;
+}
+
 void marin_gpu::destroy() {
     (void)hipStreamSynchronize(stream);
+    if (work) (void)hipFree(work);
     if (pinned) (void)hipHostFree(pinned);
     for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(stream);

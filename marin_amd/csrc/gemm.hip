@@ -1,0 +1,369 @@
+// The multi-token quantized product (prompt passes, mma.cu:52-268 of the reference redesigned): a GEMM on CDNA4's
+// int8 matrix cores with the same exact arithmetic as the decode product.
+//
+// quantize_act turns a block of activation rows into signed 8-bit limbs: per (token, quantization group) the power
+// of two 2^s that puts the group's largest magnitude in [2^29, 2^30), x 2^s rounded to an integer held exactly by
+// four limbs (x = l3 2^24 + l2 2^16 + l1 2^8 + l0), limbs stored [token][limb][column]. With an RMSNorm input the
+// limbs hold x * weight and the token's factor 1 / sqrt(mean(x^2) + eps) multiplies the token's outputs at the end.
+//
+// gemm_q8: a workgroup of 4 waves computes 128 weight rows x 32 tokens. Each wave owns two 16-row tiles and streams
+// their code windows (the A operands of v_mfma_i32_16x16x64_i8, one contiguous KiB each); the token block's limbs
+// for one group (B operands: 4 tokens x 4 limbs per 16 columns) are staged in LDS, double-buffered, and shared by
+// the 4 waves. Per group: int32 sums, converted once, scaled by weight scale x 2^-s of the token, accumulated in f32.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "gemm.hpp"
+
+namespace marin {
+
+namespace {
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int QA_THREADS = 256;
+constexpr int GM_WAVES = 4;
+constexpr int GM_ROW_TILES = 2;   // 16-row tiles per wave
+constexpr int GM_TOKENS = 32;     // tokens per workgroup
+constexpr int GM_TT = GM_TOKENS / 4;  // token tiles of 4 (one MFMA's 16 B columns)
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+}  // namespace
+
+// One token row per workgroup. GCOLS = quantization group width (a multiple of 4, at most 4 * 64).
+template <int GCOLS>
+__global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, int8_t *__restrict__ limbs,
+                                                           float *__restrict__ exps, float *__restrict__ rs_out) {
+    constexpr int TPG = GCOLS / 4;  // threads per group, 4 consecutive columns each
+    static_assert(TPG <= 64 && (TPG & (TPG - 1)) == 0, "group width");
+    __shared__ float red[QA_THREADS / 64];
+    const int t = blockIdx.x;
+    const int groups = cols / GCOLS;
+    auto load4 = [&](int k, float v[4]) {
+        if (in.mode == IN_BF16) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(in.x) + (size_t)t * in.x_stride + k);
+            v[0] = __uint_as_float(u.x << 16);
+            v[1] = __uint_as_float(u.x & 0xffff0000u);
+            v[2] = __uint_as_float(u.y << 16);
+            v[3] = __uint_as_float(u.y & 0xffff0000u);
+        } else {
+            const float4 f = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(in.x) + (size_t)t * in.x_stride + k);
+            v[0] = f.x;
+            v[1] = f.y;
+            v[2] = f.z;
+            v[3] = f.w;
+        }
+    };
+    const bool norm = in.mode == IN_NORM;
+    float rs = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+        for (int k = threadIdx.x * 4; k < cols; k += QA_THREADS * 4) {
+            float v[4];
+            load4(k, v);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < QA_THREADS / 64; ++w) total += red[w];
+        rs = 1.0f / sqrtf(total / (float)cols + in.eps);
+    }
+    if (threadIdx.x == 0) rs_out[t] = rs;
+    constexpr int GPI = QA_THREADS / TPG;  // groups per iteration
+    for (int g0 = 0; g0 < groups; g0 += GPI) {
+        const int g = g0 + (int)threadIdx.x / TPG;
+        const int k = g * GCOLS + ((int)threadIdx.x % TPG) * 4;
+        const bool on = g < groups;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (on) {
+            load4(k, v);
+            if (norm) {
+                const float4 w = *reinterpret_cast<const float4 *>(in.norm + k);
+                v[0] *= w.x;
+                v[1] *= w.y;
+                v[2] *= w.z;
+                v[3] *= w.w;
+            }
+        }
+        float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        for (int o = 1; o < TPG; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        int sh = 0;
+        if (mx > 0.0f && mx < INFINITY) {
+            int e;
+            (void)frexpf(mx, &e);
+            sh = 30 - e;
+            sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+        }
+        if (!on) continue;
+        const float up = ldexpf(1.0f, sh);
+        uint32_t word[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int xi = __float2int_rn(v[e] * up);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int lb = l == 3 ? xi : (int)(int8_t)(xi & 0xff);
+                word[l] |= ((uint32_t)lb & 0xffu) << (8 * e);
+                xi = (xi - lb) >> 8;
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+            *reinterpret_cast<uint32_t *>(limbs + ((size_t)t * 4 + l) * cols + k) = word[l];
+        if ((threadIdx.x % TPG) == 0) exps[(size_t)t * groups + g] = ldexpf(1.0f, -sh);
+    }
+}
+
+// WG: 64-column windows per group. Grid: (row blocks of 128, token blocks of 32).
+template <int WG, typename ST>
+__global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restrict__ codes,
+                                                         const ST *__restrict__ scales,
+                                                         const int8_t *__restrict__ limbs,
+                                                         const float *__restrict__ exps,
+                                                         const float *__restrict__ rsv, GemvOut out, int tokens,
+                                                         int rows, int cols, int tiles) {
+    // B fragments of one group: [buffer][window][token tile][64 lanes] x 16 bytes, and the tokens' group factors
+    __shared__ u32x4 bl[2][WG][GM_TT][64];
+    __shared__ float ex[2][GM_TOKENS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, q = lane >> 4;
+    const int windows = cols >> 6;
+    const int groups = windows / WG;
+    const int t0 = blockIdx.y * GM_TOKENS;
+    const int tile0 = (blockIdx.x * GM_WAVES + wave) * GM_ROW_TILES;
+    const size_t tile_bytes = (size_t)16 * cols;
+
+    // staging of a group's B fragments: piece p = (window, token tile, lane) of the group, 16 bytes each
+    constexpr int PIECES = WG * GM_TT * 64;
+    constexpr int PPT = PIECES / (64 * GM_WAVES);  // pieces per thread
+    struct BStage {
+        u32x4 v[PPT];
+        float e;
+    };
+    struct AStage {
+        u32x4 a[GM_ROW_TILES][WG];
+        floatx4 sc[GM_ROW_TILES];
+    };
+    auto b_load = [&](int g, BStage &st) {
+        g = min(g, groups - 1);
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = threadIdx.x + i * 64 * GM_WAVES;
+            const int w = p / (GM_TT * 64), j = (p / 64) % GM_TT, ln = p % 64;
+            const int tok = min(t0 + 4 * j + (ln & 15) / 4, tokens - 1);
+            const int limb = (ln & 15) % 4;
+            const int col = 64 * (g * WG + w) + 16 * (ln >> 4);
+            st.v[i] = *reinterpret_cast<const u32x4 *>(limbs + ((size_t)tok * 4 + limb) * cols + col);
+        }
+        st.e = exps[(size_t)min(t0 + (int)(threadIdx.x % GM_TOKENS), tokens - 1) * groups + g];
+    };
+    auto b_store = [&](int buf, const BStage &st) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = threadIdx.x + i * 64 * GM_WAVES;
+            const int w = p / (GM_TT * 64), j = (p / 64) % GM_TT, ln = p % 64;
+            bl[buf][w][j][ln] = st.v[i];
+        }
+        if (threadIdx.x < GM_TOKENS) ex[buf][threadIdx.x] = st.e;
+    };
+    // A operands (codes) and weight scales of a group for the wave's tiles (clamped to a real tile and group)
+    auto a_load = [&](int g, AStage &st) {
+        g = min(g, groups - 1);
+#pragma unroll
+        for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
+            const int tl = min(tile0 + rt, tiles - 1);
+            const uint8_t *base = codes + (size_t)tl * tile_bytes + 16 * lane;
+#pragma unroll
+            for (int w = 0; w < WG; ++w)
+                st.a[rt][w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + (size_t)(g * WG + w) * 1024));
+            const ST *sp = scales + ((size_t)tl * groups + g) * 16 + 4 * q;
+            if constexpr (sizeof(ST) == 4) {
+                st.sc[rt] = *reinterpret_cast<const floatx4 *>(sp);
+            } else {
+                const uint2 sv = *reinterpret_cast<const uint2 *>(sp);
+                st.sc[rt] = (floatx4){__uint_as_float(sv.x << 16), __uint_as_float(sv.x & 0xffff0000u),
+                                      __uint_as_float(sv.y << 16), __uint_as_float(sv.y & 0xffff0000u)};
+            }
+        }
+    };
+
+    floatx4 total[GM_ROW_TILES][GM_TT];
+#pragma unroll
+    for (int rt = 0; rt < GM_ROW_TILES; ++rt)
+#pragma unroll
+        for (int j = 0; j < GM_TT; ++j) total[rt][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+
+    // One group: MFMAs with A from registers and B from LDS buffer `buf`, then the group's scaling.
+    auto compute = [&](int buf, const AStage &as) {
+        int4v acc[GM_ROW_TILES][GM_TT];
+#pragma unroll
+        for (int rt = 0; rt < GM_ROW_TILES; ++rt)
+#pragma unroll
+            for (int j = 0; j < GM_TT; ++j) acc[rt][j] = (int4v){0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < WG; ++w) {
+#pragma unroll
+            for (int j = 0; j < GM_TT; ++j) {
+                const int4v bfrag = __builtin_bit_cast(int4v, bl[buf][w][j][lane]);
+#pragma unroll
+                for (int rt = 0; rt < GM_ROW_TILES; ++rt)
+                    acc[rt][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, as.a[rt][w]), bfrag,
+                                                                       acc[rt][j], 0, 0, 0);
+            }
+        }
+        // lane (q, c): rows 4q..4q+3 of each tile, token 4j + c/4, limb c%4
+#pragma unroll
+        for (int j = 0; j < GM_TT; ++j) {
+            const float tf = ex[buf][4 * j + c / 4];
+#pragma unroll
+            for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
+                const floatx4 f = (floatx4){(float)acc[rt][j][0], (float)acc[rt][j][1], (float)acc[rt][j][2],
+                                            (float)acc[rt][j][3]};
+                total[rt][j] += f * (as.sc[rt] * tf);
+            }
+        }
+    };
+
+    // Pipeline, two groups ahead: at iteration g, LDS buffer g%2 holds B(g), A(g) is in registers; B(g+1) and
+    // A(g+1) are in flight; the iteration issues B(g+2), computes g, issues A(g+2) into the registers A(g) held,
+    // stores B(g+1) into the other buffer and meets the other waves. Unrolled by two so every register ring index
+    // is static.
+    AStage ra[2];
+    BStage rb[2];
+    a_load(0, ra[0]);
+    b_load(0, rb[0]);
+    a_load(1, ra[1]);
+    b_load(1, rb[1]);
+    b_store(0, rb[0]);
+    __syncthreads();
+    auto iteration = [&](int g, AStage &a_now, BStage &b_free, BStage &b_next) {
+        b_load(g + 2, b_free);
+        compute(g & 1, a_now);
+        a_load(g + 2, a_now);
+        b_store((g + 1) & 1, b_next);
+        __syncthreads();
+    };
+    for (int g = 0; g < groups; g += 2) {
+        iteration(g, ra[0], rb[0], rb[1]);
+        if (g + 1 < groups) iteration(g + 1, ra[1], rb[1], rb[0]);
+    }
+
+    // limbs weighted 2^(8 l) and summed over the four lanes of a token, then the outputs
+    const float lw = (c & 3) == 0 ? 1.0f : (c & 3) == 1 ? 256.0f : (c & 3) == 2 ? 65536.0f : 16777216.0f;
+#pragma unroll
+    for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
+        const int tile = tile0 + rt;
+#pragma unroll
+        for (int j = 0; j < GM_TT; ++j) {
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float x = total[rt][j][k] * lw;
+                x += __shfl_xor(x, 1);
+                x += __shfl_xor(x, 2);
+                v[k] = x;
+            }
+            const int tok = t0 + 4 * j + c / 4;
+            if ((c & 3) != 0 || tok >= tokens || tile >= tiles) continue;
+            const float r = rsv[tok];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] *= r;
+            const int row0 = tile * 16 + 4 * q;
+            if (out.mode == OUT_SILU) {
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) {
+                    const int row = row0 + k;
+                    if (row < rows)
+                        reinterpret_cast<float *>(out.y)[(size_t)tok * out.y_stride + (row >> 1)] = silu_f(v[k]) * v[k + 1];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int row = row0 + k;
+                    if (row >= rows) continue;
+                    const size_t at = (size_t)tok * out.y_stride + row;
+                    if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v[k];
+                    else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v[k];
+                    else {
+                        const unsigned uu = __float_as_uint(v[k]);
+                        reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
+                            (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
+                                                             : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+                    }
+                }
+            }
+        }
+    }
+}
+
+bool gemm_supported(const marin_quant_matrix *w, size_t tokens) {
+    return tokens >= GEMM_MIN_TOKENS && w->bits == 8 && w->windowed && (w->group == 64 || w->group == 128) &&
+           w->cols % w->group == 0;
+}
+
+template <int WG, typename ST>
+static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
+                     const float *rs, const GemvOut &out, size_t tokens) {
+    const int tiles = (int)(w->rows_padded / 16);
+    const int rows_per_block = GM_WAVES * GM_ROW_TILES * 16;
+    dim3 grid((unsigned)((w->rows_padded + rows_per_block - 1) / rows_per_block),
+              (unsigned)((tokens + GM_TOKENS - 1) / GM_TOKENS));
+    gemm_q8<WG, ST><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
+                                                                 (int)tokens, (int)w->rows, (int)w->cols, tiles);
+}
+
+void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
+    if (!gemm_supported(w, tokens)) unsupported("matrix-core GEMM layout (int8, group 64 or 128)", 128, w->group);
+    const size_t cols = w->cols, groups = w->groups();
+    // workspace: limbs [tokens][4][cols] | exps [tokens][groups] | rs [tokens]
+    const size_t limb_bytes = (tokens * 4 * cols + 15) / 16 * 16;
+    const size_t exp_bytes = (tokens * groups * 4 + 15) / 16 * 16;
+    uint8_t *ws = (uint8_t *)g->workspace(limb_bytes + exp_bytes + tokens * 4);
+    int8_t *limbs = (int8_t *)ws;
+    float *exps = (float *)(ws + limb_bytes);
+    float *rs = (float *)(ws + limb_bytes + exp_bytes);
+    if (w->group == 128) quantize_act<128><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    else quantize_act<64><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    g->launched();
+    const bool wg2 = w->group == 128;
+    if (w->bf16_scales) {
+        if (wg2) launch_t<2, uint16_t>(g, w, limbs, exps, rs, out, tokens);
+        else launch_t<1, uint16_t>(g, w, limbs, exps, rs, out, tokens);
+    } else {
+        if (wg2) launch_t<2, float>(g, w, limbs, exps, rs, out, tokens);
+        else launch_t<1, float>(g, w, limbs, exps, rs, out, tokens);
+    }
+    const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;
+    const double outs = out.mode == OUT_SILU ? (double)w->rows / 2 : (double)w->rows;
+    const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * groups * (w->bf16_scales ? 2 : 4) +
+                         (double)tokens * cols * act + (double)tokens * outs * res;
+    g->launched(marin_gpu::GEMV, bytes, "gemm_q8");
+}
+
+void launch_product(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
+    if (!tokens) return;
+    if (gemm_supported(w, tokens) && !out.argmax) {
+        launch_gemm(g, w, in, out, tokens);
+        return;
+    }
+    const size_t in_es = in.mode == IN_BF16 ? 2 : 4, out_es = out.mode == OUT_BF16 ? 2 : 4;
+    for (size_t t0 = 0; t0 < tokens; t0 += GEMV_TOKENS) {
+        const size_t nt = std::min<size_t>(GEMV_TOKENS, tokens - t0);
+        GemvIn i2 = in;
+        i2.x = (const uint8_t *)in.x + t0 * in.x_stride * in_es;
+        GemvOut o2 = out;
+        o2.y = (uint8_t *)out.y + t0 * out.y_stride * out_es;
+        launch_gemv(g, w, i2, o2, nt);
+    }
+}
+
+}  // namespace marin

@@ -22,13 +22,14 @@
 
 #include "attention.hpp"
 #include "ops.hpp"
+#include "gemm.hpp"
 #include "gemv.hpp"
 
 using namespace marin;
 
 namespace marin {
 
-constexpr size_t CHUNK = GEMV_TOKENS;  // tokens per pass through the layers
+constexpr size_t CHUNK = 64;  // tokens per prompt pass through the layers (the products run as GEMMs)
 
 // One decode step's bookkeeping, after the output head left the greedy choice in *best as (total-order key, ~id)
 // (sampler/src/lib.rs:40-48: largest logit, lowest id on ties): record the token, clear the choice for the next
@@ -200,7 +201,8 @@ static void free_cache_graph(marin_qwen3_cache *c) {
 // One pass over `n` (<= CHUNK) tokens at the position in c->state, whose embeddings are already in c->hidden. Writes
 // the last token's logits and its greedy choice. `max_ctx` bounds the context for the attention grid; `host_ctx`
 // (when known) only feeds launch accounting.
-static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx, size_t host_ctx = 0) {
+static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx, size_t host_ctx = 0,
+                 bool head_out = true) {
     marin_gpu *g = m->gpu;
     const auto &cfg = m->cfg;
     const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd(), F = cfg.ffn;
@@ -216,7 +218,7 @@ static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx,
         qkv_out.mode = OUT_F32;
         qkv_out.y = c->qkv;
         qkv_out.y_stride = qd + 2 * kvd;
-        launch_gemv(g, L.qkv, norm_in, qkv_out, n);
+        launch_product(g, L.qkv, norm_in, qkv_out, n);
         const KvGeom geom = c->kv->geom(l);
         AttentionArgs a{};
         a.q = nullptr;
@@ -250,20 +252,21 @@ static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx,
         add_out.mode = OUT_ADD;
         add_out.y = c->hidden;
         add_out.y_stride = H;
-        launch_gemv(g, L.o, ctx_in, add_out, n);
+        launch_product(g, L.o, ctx_in, add_out, n);
         GemvIn post_in = norm_in;
         post_in.norm = L.post_norm;
         GemvOut silu_out;
         silu_out.mode = OUT_SILU;
         silu_out.y = c->act;
         silu_out.y_stride = F;
-        launch_gemv(g, L.gate_up, post_in, silu_out, n);
+        launch_product(g, L.gate_up, post_in, silu_out, n);
         GemvIn act_in;
         act_in.mode = IN_F32;
         act_in.x = c->act;
         act_in.x_stride = F;
-        launch_gemv(g, L.down, act_in, add_out, n);
+        launch_product(g, L.down, act_in, add_out, n);
     }
+    if (!head_out) return;  // a prompt's earlier chunks need no logits
     GemvIn last;
     last.mode = IN_NORM;
     last.x = c->hidden + (n - 1) * H;
@@ -295,7 +298,7 @@ static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids
         embed_device_ids<<<dim3((unsigned)nt), dim3(256), 0, g->stream>>>(
             m->embed->codes, (const float *)m->embed->scales, c->ids, c->hidden, (int)m->cfg.hidden, (int)m->cfg.group);
         g->launched();
-        pass(m, c, nt, start + t0 + nt);
+        pass(m, c, nt, start + t0 + nt, 0, t0 + nt == n);
         c->kv->len = start + t0 + nt;
     }
 }

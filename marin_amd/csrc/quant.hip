@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "gemm.hpp"
 #include "gemv.hpp"
 
 namespace marin {
@@ -305,18 +306,15 @@ void matmul_f32(marin_gpu *g, const marin_quant_matrix *w, const float *x, size_
         launch_gemv_valu(g, w, x, tokens, y);
         return;
     }
-    for (size_t t0 = 0; t0 < tokens; t0 += GEMV_TOKENS) {
-        const size_t nt = std::min<size_t>(GEMV_TOKENS, tokens - t0);
-        GemvIn in;
-        in.mode = IN_F32;
-        in.x = x + t0 * w->cols;
-        in.x_stride = w->cols;
-        GemvOut out;
-        out.mode = OUT_F32;
-        out.y = y + t0 * w->rows;
-        out.y_stride = w->rows;
-        launch_gemv(g, w, in, out, nt);
-    }
+    GemvIn in;
+    in.mode = IN_F32;
+    in.x = x;
+    in.x_stride = w->cols;
+    GemvOut out;
+    out.mode = OUT_F32;
+    out.y = y;
+    out.y_stride = w->rows;
+    launch_product(g, w, in, out, tokens);
 }
 
 }  // namespace marin
@@ -446,18 +444,15 @@ marin_status marin_matmul_quant_bf16(marin_gpu *g, const marin_quant_matrix *w, 
         check_matmul(w, x, tokens, out, MARIN_BF16);
         if (!tokens || !w->rows || !w->cols) return;
         if (!gemv_supported(w)) unsupported("bf16 product layout (group and cols multiples of 64)", 64, w->group);
-        for (size_t t0 = 0; t0 < tokens; t0 += GEMV_TOKENS) {
-            const size_t nt = std::min<size_t>(GEMV_TOKENS, tokens - t0);
-            GemvIn in;
-            in.mode = IN_BF16;
-            in.x = (const uint16_t *)x->data + t0 * w->cols;
-            in.x_stride = w->cols;
-            GemvOut o;
-            o.mode = OUT_BF16;
-            o.y = (uint16_t *)out->data + t0 * w->rows;
-            o.y_stride = w->rows;
-            launch_gemv(g, w, in, o, nt);
-        }
+        GemvIn in;
+        in.mode = IN_BF16;
+        in.x = x->data;
+        in.x_stride = w->cols;
+        GemvOut o;
+        o.mode = OUT_BF16;
+        o.y = out->data;
+        o.y_stride = w->rows;
+        launch_product(g, w, in, o, tokens);
     });
 }
 
