@@ -51,38 +51,73 @@ class Qwen3:
             check(lib.marin_qwen3_new_synthetic(gpu.handle, C.byref(self._cfg), seed, C.byref(h)))
         self._h = h
 
+    @staticmethod
+    def shape_from_hf(hf_config: dict, group: int) -> dict:
+        """The model shape from an HF config.json (model/src/qwen3/config.rs:1-330; rope_theta may sit in
+        rope_parameters, config.rs:87-90)."""
+        hd = hf_config.get("head_dim", hf_config["hidden_size"] // hf_config["num_attention_heads"])
+        rp = hf_config.get("rope_parameters") or {}
+        return dict(layers=hf_config["num_hidden_layers"], hidden=hf_config["hidden_size"],
+                    heads=hf_config["num_attention_heads"], kv_heads=hf_config["num_key_value_heads"],
+                    head_dim=hd, ffn=hf_config["intermediate_size"], vocab=hf_config["vocab_size"],
+                    eps=hf_config["rms_norm_eps"], theta=rp.get("rope_theta", hf_config.get("rope_theta", 1e4)),
+                    tied=bool(hf_config.get("tie_word_embeddings", False)), group=group)
+
+    LAYER_MATRICES = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                      "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+    LAYER_VECTORS = ("input_layernorm", "post_attention_layernorm", "self_attn.q_norm", "self_attn.k_norm")
+
     @classmethod
     def from_hf(cls, gpu: Gpu, hf_config: dict, weights: dict, quantize, group: int) -> "Qwen3":
         """Loads HF-named f32 weights, quantizing every matrix int8 with ``quantize(bf16_bits, rows, cols, bits,
         group) -> (codes, scales)`` (tensor::quantize's contract)."""
-        hd = hf_config.get("head_dim", hf_config["hidden_size"] // hf_config["num_attention_heads"])
-        rp = hf_config.get("rope_parameters") or {}
-        shape = dict(layers=hf_config["num_hidden_layers"], hidden=hf_config["hidden_size"],
-                     heads=hf_config["num_attention_heads"], kv_heads=hf_config["num_key_value_heads"],
-                     head_dim=hd, ffn=hf_config["intermediate_size"], vocab=hf_config["vocab_size"],
-                     eps=hf_config["rms_norm_eps"], theta=rp.get("rope_theta", hf_config.get("rope_theta", 1e4)),
-                     tied=bool(hf_config.get("tie_word_embeddings", False)), group=group)
+        shape = cls.shape_from_hf(hf_config, group)
         m = cls(gpu, shape)
-        from_f32 = _bf16_bits
 
         def put(layer, tensor, name):
             w = np.asarray(weights[name], np.float32)
             rows, cols = w.shape
-            codes, scales = quantize(from_f32(w).ravel(), rows, cols, 8, group)
+            codes, scales = quantize(_bf16_bits(w).ravel(), rows, cols, 8, group)
             m.load_matrix(layer, tensor, rows, cols, codes, scales)
 
         for i in range(shape["layers"]):
             p = f"model.layers.{i}."
-            for t, n in enumerate(("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
-                                   "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")):
+            for t, n in enumerate(cls.LAYER_MATRICES):
                 put(i, t, p + n + ".weight")
-            for v, n in enumerate(("input_layernorm", "post_attention_layernorm", "self_attn.q_norm",
-                                   "self_attn.k_norm")):
+            for v, n in enumerate(cls.LAYER_VECTORS):
                 m.load_vector(i, v, weights[p + n + ".weight"])
         put(-1, 0, "model.embed_tokens.weight")
         if not shape["tied"]:
             put(-1, 1, "lm_head.weight")
         m.load_vector(-1, 0, weights["model.norm.weight"])
+        return m
+
+    @classmethod
+    def from_packed(cls, gpu: Gpu, directory: str, verify: bool = True) -> "Qwen3":
+        """Loads a marin-q8-v1 artifact (GpuStore::packed, model/src/qwen3/gpu.rs:47-50): the reference's own int8
+        codes and f32 scales are uploaded as they are, with no requantization."""
+        from .packed import PackedError, open_packed
+
+        pw = open_packed(directory, verify)
+        if pw.manifest["architecture"] != "qwen3":
+            raise PackedError(f"a {pw.manifest['architecture']} artifact is not a Qwen3 model")
+        shape = cls.shape_from_hf(pw.config, pw.group)
+        m = cls(gpu, shape)
+
+        def put(layer, tensor, name):
+            rows, cols, codes, scales = pw.matrix(name)
+            m.load_matrix(layer, tensor, rows, cols, codes, scales)
+
+        for i in range(shape["layers"]):
+            p = f"model.layers.{i}."
+            for t, n in enumerate(cls.LAYER_MATRICES):
+                put(i, t, p + n + ".weight")
+            for v, n in enumerate(cls.LAYER_VECTORS):
+                m.load_vector(i, v, pw.vector(p + n + ".weight"))
+        put(-1, 0, "model.embed_tokens.weight")
+        if not shape["tied"]:
+            put(-1, 1, "lm_head.weight")
+        m.load_vector(-1, 0, pw.vector("model.norm.weight"))
         return m
 
     def load_matrix(self, layer, tensor, rows, cols, codes, scales):

@@ -138,3 +138,24 @@ def test_profiled_step_accounts_every_launch(gpu):
     # one attention launch per layer: q/k norm, RoPE, the cache store and the chunk merge happen inside it
     assert p["attention_launches"] == L
     assert p["gemv_bytes"] > 0 and p["gemv_seconds"] > 0 and p["step_seconds"] >= p["gemv_seconds"]
+
+
+def test_a_packed_artifact_loads_the_same_model_as_quantizing_on_load(gpu, tmp_path):
+    """marin-q8-v1 (loader/src/packed.rs, GpuStore::packed gpu.rs:47-50): the reference's own codes and scales,
+    uploaded as they are, give exactly the logits of quantizing the same bf16 weights on load."""
+    import shutil
+
+    from packed_bundle import write_packed
+
+    cfg, w, ref = tiny()
+    src = tmp_path / "src"
+    src.mkdir()
+    shutil.copyfile(os.path.join(GOLDEN, "tiny-qwen3", "config.json"), src / "config.json")
+    (src / "tokenizer.json").write_text('{"version": "1.0"}')
+    write_packed(str(src), w, str(tmp_path / "packed"), 64)
+    packed = Qwen3.from_packed(gpu, str(tmp_path / "packed"))
+    direct = Qwen3.from_hf(gpu, cfg, w, o.quantize, group=64)
+    prompt = ref["cases"][0]["prompt_ids"]
+    a = packed.forward(prompt, packed.new_cache(64))
+    b = direct.forward(prompt, direct.new_cache(64))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
