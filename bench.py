@@ -75,6 +75,76 @@ def cpu_baseline(shape: dict, ctx: int, budget_s: float = 12.0) -> dict:
             "seconds_per_token": round(per_token, 4)}
 
 
+MOE = {"layers": 48, "hidden": 2048, "experts": 128, "ffn": 768, "k": 8, "group": 128}
+
+
+def bench_moe(m, args) -> int:
+    """Config 4: per layer, router logits from random-init N(0, 0.02) router weights and N(0, 1) hidden states
+    (host), softmax top-8 routing on the GPU, then the timed region: the 48 layers' expert FFNs (RMSNorm, stacked
+    gate_up product over the selected experts' tiles with SiLU(gate) * up, grouped down product weighted into the
+    residual) captured as one HIP graph and replayed. Algorithmic bytes per layer: codes and f32 scales of the
+    union of the experts the batch selects (each read once by an ideal kernel)."""
+    c = MOE
+    gpu = m.Gpu()
+    H, E, F, K, L, G = c["hidden"], c["experts"], c["ffn"], c["k"], c["layers"], c["group"]
+    print(f"[bench] moe: {L} layers, {E} experts x ffn {F}, top-{K}, hidden {H}, int8 g{G}", file=sys.stderr,
+          flush=True)
+    t = time.perf_counter()
+    gate_ups = [gpu.quantized_synthetic(E * 2 * F, H, G, args.seed, 2 * l) for l in range(L)]
+    downs = [gpu.quantized_synthetic(E * H, F, G, args.seed, 2 * l + 1) for l in range(L)]
+    gpu.synchronize()
+    print(f"[bench] experts built in {time.perf_counter() - t:.1f}s", file=sys.stderr, flush=True)
+    expert_bytes = 3 * F * H * (1 + 4 / G)
+    rng = np.random.default_rng(args.seed)
+    norm = gpu.upload((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    results = {}
+    for batch in (1, 8):
+        x = rng.standard_normal((batch, H)).astype(np.float32)
+        router = (0.02 * rng.standard_normal((L, E, H))).astype(np.float32)
+        logits = np.einsum("leh,bh->lbe", router, x).astype(np.float32)
+        ids = gpu.typed(m.Dtype.U32, L * batch * K)
+        wts = gpu.zeros(L * batch * K)
+        for l in range(L):
+            li, lw = gpu.typed(m.Dtype.U32, batch * K), gpu.zeros(batch * K)
+            gpu.moe_route(gpu.upload(logits[l].ravel()), batch, E, K, True, li, lw)
+            gpu.copy_into_range(lw, wts, l * batch * K)
+            host_ids = gpu.download_typed(li)
+            results.setdefault(batch, {"ids": []})["ids"].append(host_ids)
+        ids = gpu.typed(m.Dtype.U32, host=np.concatenate(results[batch]["ids"]))
+        act = gpu.zeros(batch * K * F)
+        out = gpu.zeros(batch * H)
+        xb = gpu.upload(x.ravel())
+        sec = gpu.moe_stack_time(gate_ups, downs, xb, norm, 1e-6, ids, wts, batch, E, K, act, out,
+                                 reps=max(args.steps // 16, 5))
+        union = sum(len(np.unique(i)) for i in results[batch]["ids"])
+        selected = L * batch * K
+        algo = union * expert_bytes
+        results[batch] = {"us_per_stack": round(sec * 1e6, 1), "us_per_layer": round(sec * 1e6 / L, 2),
+                          "experts_read_per_layer": round(union / L, 2), "selections_per_layer": selected // L,
+                          "algorithmic_bytes_per_stack": round(algo), "GBps": round(algo / sec / 1e9, 1),
+                          "GBps_per_selection": round(selected * expert_bytes / sec / 1e9, 1),
+                          "tok_s_expert_stack": round(batch / sec, 1)}
+        print(f"[bench] moe batch {batch}: {sec * 1e6:.1f} us per {L}-layer stack, {union / L:.1f} experts/layer, "
+              f"{algo / sec / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+    r1 = results[1]
+    line = {
+        "metric": "grouped-expert GEMV GB/s, Qwen3-30B-A3B-shape int8 MoE layer stack",
+        "value": r1["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": max(args.steps // 16, 5), "warmup": 1,
+        "ms_per_step": round(r1["us_per_stack"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (random-init N(0,0.02) experts quantized int8 g128 on device; N(0,1) hidden states; "
+                "random-init router weights)",
+        "config": {"workload": "qwen3-30b-a3b expert FFN stack (48 layers, 128 experts x ffn 768, top-8, hidden "
+                               "2048), batch 1; batch 8 under batches", **c},
+        "roofline": {"bound": "hbm", "kernel": "gemv_decode (tile-mapped) + expert_down", "achieved": r1["GBps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(r1["GBps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": None},
+        "batches": results,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,6 +160,9 @@ def main() -> int:
                          "dispatches); mean launch durations then come from the profiled steps' events")
     ap.add_argument("--probe-copy", type=float, default=0.0, metavar="MB",
                     help="only run the bandwidth probe: copies of MB megabytes (for counter calibration), then exit")
+    ap.add_argument("--moe", action="store_true",
+                    help="config 4 instead: the Qwen3-30B-A3B-shaped expert FFN stack at batch 1 and 8 (grouped-expert "
+                         "GEMV GB/s), one JSON line")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's kernels one by one instead of replaying a HIP graph (for tracers)")
     args = ap.parse_args()
@@ -109,6 +182,9 @@ def main() -> int:
         print(json.dumps({"probe": "copy", "bytes": nbytes, "seconds": sec,
                           "GBps_read_plus_write": round(2 * nbytes / sec / 1e9, 1)}), flush=True)
         return 0
+
+    if args.moe:
+        return bench_moe(m, args)
 
     shape = SHAPES["qwen3-8b"]
     fmt = {"f32": m.KvFormat.F32, "f16": m.KvFormat.F16, "bf16": m.KvFormat.BF16}[args.kv]

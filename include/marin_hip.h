@@ -265,6 +265,30 @@ marin_status marin_qwen3_profile_launches(marin_qwen3 *m, marin_qwen3_cache *c, 
 marin_status marin_qwen3_time_kernel(marin_qwen3 *m, marin_qwen3_cache *c, const char *name, int reps,
                                      double *seconds_per_launch, uint32_t *launches_per_pass);
 
+/* ---- Mixture of experts (config 4, Qwen3-30B-A3B shape; no reference counterpart for Qwen3-MoE: the analogue is
+ * Granite's route/experts/mix, crates/cuda/src/granite.cu:12-118 and granite.rs:1-194) ----
+ * Routing: per token, probabilities = softmax over the `experts` logits; the k largest (lowest expert id on ties) in
+ * descending order into `ids` (u32 buffer [tokens][k]) and their probabilities into `weights` ([tokens][k]),
+ * renormalized to sum to 1 when `renorm` (norm_topk_prob). */
+marin_status marin_moe_route(marin_gpu *gpu, const marin_buffer *logits, size_t tokens, size_t experts, size_t k,
+                             int renorm, marin_buffer *ids, marin_buffer *weights);
+/* Expert FFN: gate_up is the experts' stacked [experts * 2F][H] int8 matrix (expert e's rows at e * 2F, gate and up
+ * interleaved row by row), down the stacked [experts * H][F] one. For every token t:
+ * out[t] += sum_j weights[t][j] * down_e(silu(gate_e x) * up_e x), e = ids[t][j], x = RMSNorm(x[t]) * norm when
+ * `norm` is given (eps), else x[t]. `act` is scratch of tokens * k * F floats. k <= 8, F a multiple of 64 up to
+ * 1024, groups 64 or 128. */
+marin_status marin_moe_ffn(marin_gpu *gpu, const marin_quant_matrix *gate_up, const marin_quant_matrix *down,
+                           const marin_buffer *x, const marin_buffer *norm, float eps, const marin_buffer *ids,
+                           const marin_buffer *weights, size_t tokens, size_t experts, size_t k, marin_buffer *act,
+                           marin_buffer *out);
+/* Measurement: the expert FFNs of `layers` layers (gate_ups[l], downs[l]; ids and weights [layers][tokens][k])
+ * captured into one HIP graph and replayed `reps` times between two events: mean seconds per replay. */
+marin_status marin_moe_stack_time(marin_gpu *gpu, size_t layers, const marin_quant_matrix *const *gate_ups,
+                                  const marin_quant_matrix *const *downs, const marin_buffer *x,
+                                  const marin_buffer *norm, float eps, const marin_buffer *ids,
+                                  const marin_buffer *weights, size_t tokens, size_t experts, size_t k,
+                                  marin_buffer *act, marin_buffer *out, int reps, double *seconds);
+
 /* Extension (bandwidth probe, the role of cuda/src/probe.rs:145-314): `reps` device-to-device copies of `bytes`
  * (a multiple of 16) through a plain streaming kernel; the mean seconds per copy. */
 marin_status marin_probe_copy(marin_gpu *gpu, size_t bytes, int reps, double *seconds);

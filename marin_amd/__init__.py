@@ -321,6 +321,28 @@ class Gpu:
         check(lib.marin_probe_copy(self._h, nbytes, reps, C.byref(sec)))
         return sec.value
 
+    # ---- mixture of experts (config 4; see include/marin_hip.h) ----
+    def moe_route(self, logits: Buffer, tokens: int, experts: int, k: int, renorm: bool, ids: Buffer,
+                  weights: Buffer) -> None:
+        check(lib.marin_moe_route(self._h, logits.handle, tokens, experts, k, int(renorm), ids.handle,
+                                  weights.handle))
+
+    def moe_ffn(self, gate_up: DeviceQuantMatrix, down: DeviceQuantMatrix, x: Buffer, norm, eps: float,
+                ids: Buffer, weights: Buffer, tokens: int, experts: int, k: int, act: Buffer, out: Buffer) -> None:
+        check(lib.marin_moe_ffn(self._h, gate_up._h, down._h, x.handle, norm.handle if norm is not None else None,
+                                eps, ids.handle, weights.handle, tokens, experts, k, act.handle, out.handle))
+
+    def moe_stack_time(self, gate_ups, downs, x: Buffer, norm, eps: float, ids: Buffer, weights: Buffer,
+                       tokens: int, experts: int, k: int, act: Buffer, out: Buffer, reps: int = 10) -> float:
+        n = len(gate_ups)
+        gu = (C.c_void_p * n)(*[m._h.value if hasattr(m._h, "value") else m._h for m in gate_ups])
+        dn = (C.c_void_p * n)(*[m._h.value if hasattr(m._h, "value") else m._h for m in downs])
+        sec = C.c_double()
+        check(lib.marin_moe_stack_time(self._h, n, gu, dn, x.handle, norm.handle if norm is not None else None,
+                                       eps, ids.handle, weights.handle, tokens, experts, k, act.handle, out.handle,
+                                       reps, C.byref(sec)))
+        return sec.value
+
     def embed_quant(self, table: DeviceQuantMatrix, ids, scratch: Tokens, out: Buffer) -> None:
         ids = np.ascontiguousarray(ids, np.uint32).ravel()
         check(lib.marin_embed_quant(self._h, table._h, ids.ctypes.data if ids.size else None, ids.size,

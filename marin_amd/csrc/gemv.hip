@@ -471,8 +471,9 @@ void launch_gemv(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     }
     // algorithmic bytes: codes + scales once, activations and outputs once
     const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;
-    const double outs = out.mode == OUT_SILU ? (double)w->rows / 2 : (double)w->rows;
-    const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * w->groups() * (w->bf16_scales ? 2 : 4) +
+    const double rows = in.tile_map ? 16.0 * in.map_tiles * in.map_count : (double)w->rows;  // rows read
+    const double outs = out.mode == OUT_SILU ? rows / 2 : rows;
+    const double bytes = rows * w->row_bytes() + rows * w->groups() * (w->bf16_scales ? 2 : 4) +
                          (double)tokens * w->cols * act + (double)tokens * outs * res;
     g->launched(marin_gpu::GEMV, bytes, name);
 }

@@ -25,6 +25,11 @@ struct GemvIn {
     size_t x_stride = 0;
     const float *norm = nullptr;
     float eps = 0.0f;
+    // Optional (one-token product only): the product runs over the 16-row tiles of `map_count` blocks of
+    // `map_tiles` tiles each, block j being block tile_map[j] of the matrix (device ids, e.g. selected experts);
+    // output row r of the product is logical row r of that concatenation.
+    const int32_t *tile_map = nullptr;
+    int map_tiles = 0, map_count = 0;
 };
 
 struct GemvOut {

@@ -146,7 +146,9 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     Raw ring[RING];
     floatx4 sring[RING / WG];
     auto load_item = [&](int i, int slot) {
-        const int t = (int)blockIdx.x + (i / S) * (int)gridDim.x;
+        const int tl = (int)blockIdx.x + (i / S) * (int)gridDim.x;  // logical tile
+        // mapped tiles: a wave-uniform index, so the block id comes through the scalar cache, off the vector counter
+        const int t = in.tile_map ? in.tile_map[tl / in.map_tiles] * in.map_tiles + tl % in.map_tiles : tl;
         const int w = min(w0 + i % S, windows - 1);
         const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane;
         if constexpr (BITS == 8) ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
@@ -367,7 +369,9 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
                                     std::to_string(SM) + ", " + (sizeof(ST) == 4 ? "float" : "unsigned short") + ">";
     const int windows = (int)(w->cols / 64);
     const int groups = windows / WG;
-    const int tiles = (int)(w->rows_padded / 16);
+    // a tile map makes the product's (logical) tiles the mapped blocks of tiles
+    const int tiles = in.tile_map ? in.map_tiles * in.map_count : (int)(w->rows_padded / 16);
+    const int rows = in.tile_map ? tiles * 16 : (int)w->rows;
     const size_t gpad = (size_t)((groups + 3) & ~3);
     const size_t lds = (size_t)DW * SM * 256 + gpad * 4 + (BITS == 4 ? gpad * 16 : 0) + (size_t)(2 * DW * 16 + DW) * 4;
     auto kern = gemv_decode<BITS, WG, SM, ST>;
@@ -388,10 +392,10 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     g->kernel_events(t0, t1);
     if (t0)
         hipExtLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * DW), (uint32_t)lds, g->stream, t0, t1, 0u, w->codes,
-                              (const ST *)w->scales, in, out, (int)w->rows, (int)w->cols, tiles);
+                              (const ST *)w->scales, in, out, rows, (int)w->cols, tiles);
     else
         kern<<<dim3((unsigned)blocks), dim3(64 * DW), lds, g->stream>>>(w->codes, (const ST *)w->scales, in, out,
-                                                                        (int)w->rows, (int)w->cols, tiles);
+                                                                        rows, (int)w->cols, tiles);
     return name.c_str();
 }
 
