@@ -116,6 +116,9 @@ def bench_moe(m, args) -> int:
         xb = gpu.upload(x.ravel())
         sec = gpu.moe_stack_time(gate_ups, downs, xb, norm, 1e-6, ids, wts, batch, E, K, act, out,
                                  reps=max(args.steps // 16, 5))
+        reps = max(args.steps // 16, 5)
+        parts = [gpu.moe_stack_time(gate_ups, downs, xb, norm, 1e-6, ids, wts, batch, E, K, act, out, reps=reps,
+                                    part=p) for p in (1, 2)]
         union = sum(len(np.unique(i)) for i in results[batch]["ids"])
         selected = L * batch * K
         algo = union * expert_bytes
@@ -123,9 +126,14 @@ def bench_moe(m, args) -> int:
                           "experts_read_per_layer": round(union / L, 2), "selections_per_layer": selected // L,
                           "algorithmic_bytes_per_stack": round(algo), "GBps": round(algo / sec / 1e9, 1),
                           "GBps_per_selection": round(selected * expert_bytes / sec / 1e9, 1),
-                          "tok_s_expert_stack": round(batch / sec, 1)}
+                          "tok_s_expert_stack": round(batch / sec, 1),
+                          "gate_up_us_per_layer": round(parts[0] * 1e6 / L, 2),
+                          "down_us_per_layer": round(parts[1] * 1e6 / L, 2),
+                          "gate_up_GBps": round(union * 2 * F * H * (1 + 4 / G) / parts[0] / 1e9, 1),
+                          "down_GBps": round(union * F * H * (1 + 4 / G) / parts[1] / 1e9, 1)}
         print(f"[bench] moe batch {batch}: {sec * 1e6:.1f} us per {L}-layer stack, {union / L:.1f} experts/layer, "
-              f"{algo / sec / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+              f"{algo / sec / 1e9:.0f} GB/s (gate_up {parts[0] * 1e6 / L:.1f} us/layer, down "
+              f"{parts[1] * 1e6 / L:.1f} us/layer)", file=sys.stderr, flush=True)
     r1 = results[1]
     line = {
         "metric": "grouped-expert GEMV GB/s, Qwen3-30B-A3B-shape int8 MoE layer stack",

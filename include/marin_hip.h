@@ -282,12 +282,13 @@ marin_status marin_moe_ffn(marin_gpu *gpu, const marin_quant_matrix *gate_up, co
                            const marin_buffer *weights, size_t tokens, size_t experts, size_t k, marin_buffer *act,
                            marin_buffer *out);
 /* Measurement: the expert FFNs of `layers` layers (gate_ups[l], downs[l]; ids and weights [layers][tokens][k])
- * captured into one HIP graph and replayed `reps` times between two events: mean seconds per replay. */
+ * captured into one HIP graph and replayed `reps` times between two events: mean seconds per replay. `part` 0 times
+ * the whole FFN, 1 only the gate_up products, 2 only the down products (whose inputs are then last call's `act`). */
 marin_status marin_moe_stack_time(marin_gpu *gpu, size_t layers, const marin_quant_matrix *const *gate_ups,
                                   const marin_quant_matrix *const *downs, const marin_buffer *x,
                                   const marin_buffer *norm, float eps, const marin_buffer *ids,
                                   const marin_buffer *weights, size_t tokens, size_t experts, size_t k,
-                                  marin_buffer *act, marin_buffer *out, int reps, double *seconds);
+                                  marin_buffer *act, marin_buffer *out, int part, int reps, double *seconds);
 
 /* Extension (bandwidth probe, the role of cuda/src/probe.rs:145-314): `reps` device-to-device copies of `bytes`
  * (a multiple of 16) through a plain streaming kernel; the mean seconds per copy. */

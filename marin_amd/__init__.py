@@ -333,14 +333,14 @@ class Gpu:
                                 eps, ids.handle, weights.handle, tokens, experts, k, act.handle, out.handle))
 
     def moe_stack_time(self, gate_ups, downs, x: Buffer, norm, eps: float, ids: Buffer, weights: Buffer,
-                       tokens: int, experts: int, k: int, act: Buffer, out: Buffer, reps: int = 10) -> float:
+                       tokens: int, experts: int, k: int, act: Buffer, out: Buffer, reps: int = 10, part: int = 0) -> float:
         n = len(gate_ups)
         gu = (C.c_void_p * n)(*[m._h.value if hasattr(m._h, "value") else m._h for m in gate_ups])
         dn = (C.c_void_p * n)(*[m._h.value if hasattr(m._h, "value") else m._h for m in downs])
         sec = C.c_double()
         check(lib.marin_moe_stack_time(self._h, n, gu, dn, x.handle, norm.handle if norm is not None else None,
                                        eps, ids.handle, weights.handle, tokens, experts, k, act.handle, out.handle,
-                                       reps, C.byref(sec)))
+                                       part, reps, C.byref(sec)))
         return sec.value
 
     def embed_quant(self, table: DeviceQuantMatrix, ids, scratch: Tokens, out: Buffer) -> None:

@@ -120,7 +120,7 @@ SIGNATURES = {
     "marin_probe_copy": (st, [P, sz, C.c_int, C.POINTER(C.c_double)]),
     "marin_moe_route": (st, [P, P, sz, sz, sz, C.c_int, P, P]),
     "marin_moe_ffn": (st, [P, P, P, P, P, C.c_float, P, P, sz, sz, sz, P, P]),
-    "marin_moe_stack_time": (st, [P, sz, P, P, P, P, C.c_float, P, P, sz, sz, sz, P, P, C.c_int,
+    "marin_moe_stack_time": (st, [P, sz, P, P, P, P, C.c_float, P, P, sz, sz, sz, P, P, C.c_int, C.c_int,
                                   C.POINTER(C.c_double)]),
     "marin_qwen3_time_kernel": (st, [P, P, C.c_char_p, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint32)]),
     "marin_qwen3_profile_launches": (st, [P, P, C.POINTER(LaunchRecordC), sz, C.POINTER(sz)]),

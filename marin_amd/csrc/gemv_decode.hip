@@ -3,8 +3,8 @@
 // Same arithmetic as the multi-token matrix-core product (codes are the A operand of v_mfma_i32_16x16x64_i8,
 // activations become exact signed 8-bit limbs in the B columns, int32 sums per group scaled once per group), with a
 // schedule cut down to what one token needs:
-//  - every wave owns a fixed slice of the columns (whole groups) for the whole launch, so it builds the limbs of its
-//    slice once, into LDS, and reuses them for every 16-row tile it visits;
+//  - the block builds the limbs of the whole row once, into LDS (each column loaded once per block); every wave owns
+//    a fixed slice of the columns (whole groups) for the whole launch and reuses its limbs for every 16-row tile;
 //  - the power of two that scales the activations into 30-bit integers is chosen per group of columns (from the
 //    group's largest magnitude), not per row, so no block-wide maximum is needed; it is folded into the group's
 //    weight scale;
@@ -41,7 +41,8 @@ constexpr int RING = DECODE_RING;  // code windows in flight per wave
 #ifndef DECODE_BPC
 #define DECODE_BPC 2
 #endif
-constexpr int DECODE_BLOCKS_PER_CU = DECODE_BPC;  // resident blocks the persistent grid aims at per compute unit
+constexpr int DECODE_BLOCKS_PER_CU = DECODE_BPC;
+constexpr int MAP_MAX = 64;  // tile map entries (selected experts) a launch may carry: one per lane  // resident blocks the persistent grid aims at per compute unit
 
 // Lane permutations inside rows of 16 lanes (DPP): 0xB1 swaps neighbours, 0x4E swaps pairs, 0x141 mirrors each
 // half row of 8 lanes.
@@ -118,19 +119,26 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int items = my_tiles * S;
 
-    // ---- activations of the slice first. In round r, lane L holds the 16 consecutive columns
-    // 64 w0 + 1024 r + 16 L .. + 16, i.e. quarter L % 4 of window r * 16 + L / 4 of the slice: exactly what the B
-    // operand of that window needs, so the lane builds all four limbs of its columns and stores each as 16 bytes.
-    // Four 16-byte loads per round in every mode (bf16 rows use the first two), and the norm weights always loaded
-    // (the activation address stands in when there is no norm), so no branch joins loaded values before the ring
-    // is issued: waiting for them then never drains the ring.
-    constexpr int R = (S + 15) / 16;
+    // A tile map (at most MAP_MAX entries) is loaded first, one entry per lane, and each item picks its entry with
+    // a wave-uniform lane read: a per-item load of the map would sit behind the code windows already in flight and
+    // wait for all of them.
+    const int *map_p = in.tile_map ? in.tile_map : reinterpret_cast<const int *>(in.x);
+    const int map_v = map_p[min(lane, max(in.map_count, 1) - 1)];
+
+    // ---- the activations, block-wide: in round r, thread T holds the 16 consecutive columns 8192 r + 16 T .. + 16,
+    // i.e. quarter T % 4 of window 128 r + T / 4: exactly what the B operand of that window needs, so the thread
+    // builds all four limbs of its columns and stores each as 16 bytes; every wave then reads the limbs of its own
+    // windows. Each column is loaded once per block; threads past the row's end all load the row's last 16 columns
+    // (one cache line per wave). Four 16-byte loads per round (bf16 rows use the first two) and the norm weights
+    // (the activation address stands in when there is no norm), all unconditional and issued before the code ring:
+    // with no branch around them the waits for them are exact and never drain the ring.
+    constexpr int R = (S + 15) / 16;  // rounds of 8192 columns: DW * S windows at most
     const bool norm = in.mode == IN_NORM, bf = in.mode == IN_BF16;
     const unsigned char *xb = reinterpret_cast<const unsigned char *>(in.x);
     u32x4 xr[R][4], nr[R][4];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int cb = min(w0 * 64 + r * 1024 + 16 * lane, cols - 16);
+        const int cb = min(r * 8192 + 16 * (int)threadIdx.x, cols - 16);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const size_t xo = bf ? (size_t)cb * 2 + 16 * (v & 1) : (size_t)cb * 4 + 16 * v;
@@ -147,8 +155,8 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     floatx4 sring[RING / WG];
     auto load_item = [&](int i, int slot) {
         const int tl = (int)blockIdx.x + (i / S) * (int)gridDim.x;  // logical tile
-        // mapped tiles: a wave-uniform index, so the block id comes through the scalar cache, off the vector counter
-        const int t = in.tile_map ? in.tile_map[tl / in.map_tiles] * in.map_tiles + tl % in.map_tiles : tl;
+        const int t = in.tile_map ? __builtin_amdgcn_readlane(map_v, tl / in.map_tiles) * in.map_tiles + tl % in.map_tiles
+                                  : tl;
         const int w = min(w0 + i % S, windows - 1);
         const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane;
         if constexpr (BITS == 8) ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     for (int j = 0; j < RING; ++j) load_item(min(j, last), j);
     TRACE(2);
 
-    // ---- prologue: RMSNorm statistic (the waves' slices cover the row once), then this wave's limbs
+    // ---- prologue: RMSNorm statistic (the threads' columns cover the row once), then the limbs
     float xv[R][16];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -174,16 +182,15 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             }
         }
     }
-    auto in_slice = [&](int r) {  // this lane's columns lie in the slice and in the row
-        const int wl = r * 16 + lane / 4;
-        return wl < S && w0 + wl < windows;
+    auto in_row = [&](int r) {  // this thread's columns lie in the row
+        return r * 8192 + 16 * (int)threadIdx.x < cols;
     };
     float rs = 1.0f;
     if (norm) {
         float ss = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (in_slice(r))
+            if (in_row(r))
 #pragma unroll
                 for (int e = 0; e < 16; ++e) ss += xv[r][e] * xv[r][e];
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
@@ -196,8 +203,9 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int wl = r * 16 + lane / 4;
-        const bool valid = in_slice(r);
+        if (r * 8192 + wave * 1024 >= cols) continue;  // wave-uniform: nothing loaded
+        const int wr = r * 128 + (int)threadIdx.x / 4;  // window of this thread's columns
+        const bool valid = in_row(r);
         float v[16];
         float mx = 0.0f;
 #pragma unroll
@@ -237,9 +245,9 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         if (valid) {
 #pragma unroll
             for (int l = 0; l < 4; ++l)
-                *reinterpret_cast<u32x4 *>(limbs + ((size_t)(wave * S + wl) * 4 + l) * 64 + 16 * (lane & 3)) = pk[l];
+                *reinterpret_cast<u32x4 *>(limbs + ((size_t)wr * 4 + l) * 64 + 16 * (lane & 3)) = pk[l];
         }
-        const int g = (w0 + wl) / WG;
+        const int g = wr / WG;
         if (valid && (lane & (4 * WG - 1)) == 0) gdown[g] = ldexpf(1.0f, -sh);
         if constexpr (BITS == 4) {
             // stored nibbles are code + 8: the group's sum of each limb column, times 8, comes off the sums
@@ -370,6 +378,8 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     const int windows = (int)(w->cols / 64);
     const int groups = windows / WG;
     // a tile map makes the product's (logical) tiles the mapped blocks of tiles
+    if (in.tile_map && (in.map_count < 1 || in.map_count > MAP_MAX || in.map_tiles < 1))
+        unsupported("tile map entries (1 to 64)", MAP_MAX, (size_t)in.map_count);
     const int tiles = in.tile_map ? in.map_tiles * in.map_count : (int)(w->rows_padded / 16);
     const int rows = in.tile_map ? tiles * 16 : (int)w->rows;
     const size_t gpad = (size_t)((groups + 3) & ~3);

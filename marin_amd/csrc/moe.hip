@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -278,9 +279,9 @@ static void check_moe(const MoeArgs &a) {
 
 // One or more tokens' MoE FFN: out[t] += sum_j w[t][j] down_{e}(silu(gate_e x) * up_e x), x = RMSNorm(x[t]) when a
 // norm is given.
-static void launch_moe(marin_gpu *g, const MoeArgs &a) {
+static void launch_moe(marin_gpu *g, const MoeArgs &a, int part = 0) {
     check_moe(a);
-    for (size_t t = 0; t < a.tokens; ++t) {
+    for (size_t t = 0; t < a.tokens && part != 2; ++t) {
         GemvIn in;
         in.mode = a.norm ? IN_NORM : IN_F32;
         in.x = a.x + t * a.hidden;
@@ -296,6 +297,7 @@ static void launch_moe(marin_gpu *g, const MoeArgs &a) {
         o.y_stride = a.k * a.ffn;
         launch_gemv(g, a.gate_up, in, o, 1);
     }
+    if (part == 1) return;
     if (a.down->bf16_scales)
         launch_down_st<uint16_t>(g, a.down, a.act, a.ids, a.weights, a.tokens, a.k, a.hidden, a.ffn, a.out);
     else
@@ -364,10 +366,11 @@ marin_status marin_moe_stack_time(marin_gpu *g, size_t layers, const marin_quant
                                   const marin_quant_matrix *const *downs, const marin_buffer *x,
                                   const marin_buffer *norm, float eps, const marin_buffer *ids,
                                   const marin_buffer *weights, size_t tokens, size_t experts, size_t k,
-                                  marin_buffer *act, marin_buffer *out, int reps, double *seconds) {
+                                  marin_buffer *act, marin_buffer *out, int part, int reps, double *seconds) {
     return guard([&] {
         if (!layers || !tokens) shape("layers and tokens", 1, 0);
         if (reps < 1) shape("timing repetitions", 1, (size_t)reps);
+        if (part < 0 || part > 2) shape("stack part (0 all, 1 gate_up, 2 down)", 2, (size_t)part);
         std::vector<MoeArgs> per(layers);
         for (size_t l = 0; l < layers; ++l) {
             MoeArgs &a = per[l];
@@ -389,11 +392,26 @@ marin_status marin_moe_stack_time(marin_gpu *g, size_t layers, const marin_quant
             a.out = (float *)f32_of(out, tokens * a.hidden, "output");
             check_moe(a);
         }
+        const char *ng = getenv("MARIN_NO_GRAPH");
+        if (ng && *ng && *ng != '0') {
+            // eager launches (for tracers that do not follow graph replays)
+            for (auto &a : per) launch_moe(g, a, part);
+            hipEvent_t t0 = g->next_event(), t1 = g->next_event();
+            HIP_CHECK(hipEventRecord(t0, g->stream));
+            for (int r = 0; r < reps; ++r)
+                for (auto &a : per) launch_moe(g, a, part);
+            HIP_CHECK(hipEventRecord(t1, g->stream));
+            HIP_CHECK(hipEventSynchronize(t1));
+            float ms = 0.0f;
+            HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
+            *seconds = ms * 1e-3 / reps;
+            return;
+        }
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
         HIP_CHECK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
         try {
-            for (auto &a : per) launch_moe(g, a);
+            for (auto &a : per) launch_moe(g, a, part);
         } catch (...) {
             hipGraph_t junk = nullptr;
             (void)hipStreamEndCapture(g->stream, &junk);
