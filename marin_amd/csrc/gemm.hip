@@ -28,8 +28,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int QA_THREADS = 256;
 constexpr int GM_WAVES = 4;
 constexpr int GM_ROW_TILES = 2;   // 16-row tiles per wave
-constexpr int GM_TOKENS = 32;     // tokens per workgroup
-constexpr int GM_TT = GM_TOKENS / 4;  // token tiles of 4 (one MFMA's 16 B columns)
+constexpr int GM_TOKENS = 32;     // tokens per workgroup of the prompt GEMM
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
@@ -122,29 +121,41 @@ __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, 
     }
 }
 
-// WG: 64-column windows per group. Grid: (row blocks of 128, token blocks of 32).
-template <int WG, typename ST>
+// WG: 64-column windows per group; TOK: tokens per workgroup (a multiple of 4).
+// Prompt GEMM (MOE false): grid (row blocks of 128, token blocks of TOK).
+// Grouped expert product (MOE true, gate_up of a decode batch of at most TOK tokens): grid (row blocks of 128 of
+// one expert, distinct selected experts); workgroup (x, u) computes rows 128 x .. of expert plan.experts[u] for every
+// token and writes SiLU(gate) * up of the tokens that selected it into their (token, slot) activation rows. `tiles`
+// is then the tiles of one expert.
+template <int WG, typename ST, int TOK, bool MOE>
 __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restrict__ codes,
                                                          const ST *__restrict__ scales,
                                                          const int8_t *__restrict__ limbs,
                                                          const float *__restrict__ exps,
                                                          const float *__restrict__ rsv, GemvOut out, int tokens,
-                                                         int rows, int cols, int tiles) {
+                                                         int rows, int cols, int tiles, MoePlanView plan) {
+    constexpr int TT = TOK / 4;  // token tiles of 4 (one MFMA's 16 B columns)
     // B fragments of one group: [buffer][window][token tile][64 lanes] x 16 bytes, and the tokens' group factors
-    __shared__ u32x4 bl[2][WG][GM_TT][64];
-    __shared__ float ex[2][GM_TOKENS];
+    __shared__ u32x4 bl[2][WG][TT][64];
+    __shared__ float ex[2][TOK];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q = lane >> 4;
     const int windows = cols >> 6;
     const int groups = windows / WG;
-    const int t0 = blockIdx.y * GM_TOKENS;
+    int t0 = blockIdx.y * TOK, tbase = 0;
+    if constexpr (MOE) {
+        // the whole workgroup leaves together, before any barrier
+        if ((int)blockIdx.y >= plan.plan[0]) return;
+        t0 = 0;
+        tbase = plan.plan[MOE_PLAN_EXPERTS + blockIdx.y] * tiles;  // the expert's first tile
+    }
     const int tile0 = (blockIdx.x * GM_WAVES + wave) * GM_ROW_TILES;
     const size_t tile_bytes = (size_t)16 * cols;
 
     // staging of a group's B fragments: piece p = (window, token tile, lane) of the group, 16 bytes each
-    constexpr int PIECES = WG * GM_TT * 64;
-    constexpr int PPT = PIECES / (64 * GM_WAVES);  // pieces per thread
+    constexpr int PIECES = WG * TT * 64;
+    constexpr int PPT = (PIECES + 64 * GM_WAVES - 1) / (64 * GM_WAVES);  // pieces per thread (the last clamped)
     struct BStage {
         u32x4 v[PPT];
         float e;
@@ -157,30 +168,30 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
         g = min(g, groups - 1);
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int p = threadIdx.x + i * 64 * GM_WAVES;
-            const int w = p / (GM_TT * 64), j = (p / 64) % GM_TT, ln = p % 64;
+            const int p = min((int)threadIdx.x + i * 64 * GM_WAVES, PIECES - 1);
+            const int w = p / (TT * 64), j = (p / 64) % TT, ln = p % 64;
             const int tok = min(t0 + 4 * j + (ln & 15) / 4, tokens - 1);
             const int limb = (ln & 15) % 4;
             const int col = 64 * (g * WG + w) + 16 * (ln >> 4);
             st.v[i] = *reinterpret_cast<const u32x4 *>(limbs + ((size_t)tok * 4 + limb) * cols + col);
         }
-        st.e = exps[(size_t)min(t0 + (int)(threadIdx.x % GM_TOKENS), tokens - 1) * groups + g];
+        st.e = exps[(size_t)min(t0 + (int)(threadIdx.x % TOK), tokens - 1) * groups + g];
     };
     auto b_store = [&](int buf, const BStage &st) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int p = threadIdx.x + i * 64 * GM_WAVES;
-            const int w = p / (GM_TT * 64), j = (p / 64) % GM_TT, ln = p % 64;
-            bl[buf][w][j][ln] = st.v[i];
+            const int p = (int)threadIdx.x + i * 64 * GM_WAVES;
+            const int w = p / (TT * 64), j = (p / 64) % TT, ln = p % 64;
+            if (p < PIECES) bl[buf][w][j][ln] = st.v[i];
         }
-        if (threadIdx.x < GM_TOKENS) ex[buf][threadIdx.x] = st.e;
+        if (threadIdx.x < TOK) ex[buf][threadIdx.x] = st.e;
     };
     // A operands (codes) and weight scales of a group for the wave's tiles (clamped to a real tile and group)
     auto a_load = [&](int g, AStage &st) {
         g = min(g, groups - 1);
 #pragma unroll
         for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
-            const int tl = min(tile0 + rt, tiles - 1);
+            const int tl = tbase + min(tile0 + rt, tiles - 1);
             const uint8_t *base = codes + (size_t)tl * tile_bytes + 16 * lane;
 #pragma unroll
             for (int w = 0; w < WG; ++w)
@@ -196,23 +207,23 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
         }
     };
 
-    floatx4 total[GM_ROW_TILES][GM_TT];
+    floatx4 total[GM_ROW_TILES][TT];
 #pragma unroll
     for (int rt = 0; rt < GM_ROW_TILES; ++rt)
 #pragma unroll
-        for (int j = 0; j < GM_TT; ++j) total[rt][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TT; ++j) total[rt][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
     // One group: MFMAs with A from registers and B from LDS buffer `buf`, then the group's scaling.
     auto compute = [&](int buf, const AStage &as) {
-        int4v acc[GM_ROW_TILES][GM_TT];
+        int4v acc[GM_ROW_TILES][TT];
 #pragma unroll
         for (int rt = 0; rt < GM_ROW_TILES; ++rt)
 #pragma unroll
-            for (int j = 0; j < GM_TT; ++j) acc[rt][j] = (int4v){0, 0, 0, 0};
+            for (int j = 0; j < TT; ++j) acc[rt][j] = (int4v){0, 0, 0, 0};
 #pragma unroll
         for (int w = 0; w < WG; ++w) {
 #pragma unroll
-            for (int j = 0; j < GM_TT; ++j) {
+            for (int j = 0; j < TT; ++j) {
                 const int4v bfrag = __builtin_bit_cast(int4v, bl[buf][w][j][lane]);
 #pragma unroll
                 for (int rt = 0; rt < GM_ROW_TILES; ++rt)
@@ -222,7 +233,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
         }
         // lane (q, c): rows 4q..4q+3 of each tile, token 4j + c/4, limb c%4
 #pragma unroll
-        for (int j = 0; j < GM_TT; ++j) {
+        for (int j = 0; j < TT; ++j) {
             const float tf = ex[buf][4 * j + c / 4];
 #pragma unroll
             for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
@@ -263,7 +274,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
     for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
         const int tile = tile0 + rt;
 #pragma unroll
-        for (int j = 0; j < GM_TT; ++j) {
+        for (int j = 0; j < TT; ++j) {
             float v[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -278,6 +289,16 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[k] *= r;
             const int row0 = tile * 16 + 4 * q;
+            if constexpr (MOE) {
+                // the token's slot for this expert (-1: it did not select it); rows are the expert's interleaved
+                // gate/up pairs
+                const int slot = plan.plan[MOE_PLAN_SLOTS + blockIdx.y * MOE_BATCH + tok];
+                if (slot < 0) continue;
+                float *dst = reinterpret_cast<float *>(out.y) + ((size_t)tok * plan.k + slot) * plan.ffn;
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) dst[(row0 + k) >> 1] = silu_f(v[k]) * v[k + 1];
+                continue;
+            }
             if (out.mode == OUT_SILU) {
 #pragma unroll
                 for (int k = 0; k < 4; k += 2) {
@@ -317,8 +338,9 @@ static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *li
     const int rows_per_block = GM_WAVES * GM_ROW_TILES * 16;
     dim3 grid((unsigned)((w->rows_padded + rows_per_block - 1) / rows_per_block),
               (unsigned)((tokens + GM_TOKENS - 1) / GM_TOKENS));
-    gemm_q8<WG, ST><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
-                                                                 (int)tokens, (int)w->rows, (int)w->cols, tiles);
+    gemm_q8<WG, ST, GM_TOKENS, false><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(
+        w->codes, (const ST *)w->scales, limbs, exps, rs, out, (int)tokens, (int)w->rows, (int)w->cols, tiles,
+        MoePlanView{});
 }
 
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
@@ -347,6 +369,54 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * groups * (w->bf16_scales ? 2 : 4) +
                          (double)tokens * cols * act + (double)tokens * outs * res;
     g->launched(marin_gpu::GEMV, bytes, "gemm_q8");
+}
+
+static size_t align16(size_t n) { return (n + 15) / 16 * 16; }
+
+size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group) {
+    return align16(tokens * 4 * cols) + align16(tokens * (cols / group) * 4) + tokens * 4;
+}
+
+template <int WG, typename ST>
+static void launch_moe_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
+                         const float *rs, size_t tokens, const MoePlanView &plan, size_t max_experts, float *act) {
+    const int tiles = 2 * plan.ffn / 16;  // one expert's tiles
+    const int rows_per_block = GM_WAVES * GM_ROW_TILES * 16;
+    dim3 grid((unsigned)((2 * plan.ffn + rows_per_block - 1) / rows_per_block), (unsigned)max_experts);
+    GemvOut out;
+    out.mode = OUT_SILU;
+    out.y = act;
+    gemm_q8<WG, ST, MOE_BATCH, true><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(
+        w->codes, (const ST *)w->scales, limbs, exps, rs, out, (int)tokens, 2 * plan.ffn, (int)w->cols, tiles, plan);
+}
+
+void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, size_t tokens,
+                        const int32_t *plan, size_t max_experts, size_t k, size_t ffn, float *act) {
+    if (tokens < 1 || tokens > (size_t)MOE_BATCH) unsupported("tokens of a grouped expert batch", MOE_BATCH, tokens);
+    if (max_experts > (size_t)MOE_PLAN_MAX) unsupported("distinct experts of a batch", MOE_PLAN_MAX, max_experts);
+    if (w->bits != 8 || !w->windowed || !(w->group == 64 || w->group == 128) || w->cols % w->group)
+        unsupported("grouped expert layout (int8, group 64 or 128)", 128, w->group);
+    const size_t cols = w->cols, groups = w->groups();
+    const size_t limb_bytes = align16(tokens * 4 * cols), exp_bytes = align16(tokens * groups * 4);
+    uint8_t *ws = (uint8_t *)g->workspace(moe_gate_up_workspace(tokens, cols, w->group));
+    int8_t *limbs = (int8_t *)ws;
+    float *exps = (float *)(ws + limb_bytes);
+    float *rs = (float *)(ws + limb_bytes + exp_bytes);
+    if (w->group == 128) quantize_act<128><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    else quantize_act<64><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    g->launched();
+    MoePlanView pv;
+    pv.plan = plan;
+    pv.k = (int)k;
+    pv.ffn = (int)ffn;
+    const bool wg2 = w->group == 128;
+    if (w->bf16_scales) {
+        if (wg2) launch_moe_t<2, uint16_t>(g, w, limbs, exps, rs, tokens, pv, max_experts, act);
+        else launch_moe_t<1, uint16_t>(g, w, limbs, exps, rs, tokens, pv, max_experts, act);
+    } else {
+        if (wg2) launch_moe_t<2, float>(g, w, limbs, exps, rs, tokens, pv, max_experts, act);
+        else launch_moe_t<1, float>(g, w, limbs, exps, rs, tokens, pv, max_experts, act);
+    }
 }
 
 void launch_product(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {

@@ -7,11 +7,32 @@ namespace marin {
 
 constexpr size_t GEMM_MIN_TOKENS = 16;  // token counts from which the GEMM replaces chunks of the decode product
 
+// The routing plan of a decode batch's MoE layer (device int32 words, written by moe_plan): [0] the count U of
+// distinct selected experts; [MOE_PLAN_EXPERTS + u] the u-th smallest of them; [MOE_PLAN_SLOTS + u * MOE_BATCH + t]
+// the slot j with ids[t][j] == that expert, or -1.
+constexpr int MOE_PLAN_MAX = 64;  // distinct experts of a batch: tokens x k
+constexpr int MOE_BATCH = 8;      // tokens of a grouped batch
+constexpr int MOE_PLAN_EXPERTS = 1;
+constexpr int MOE_PLAN_SLOTS = 1 + MOE_PLAN_MAX;
+constexpr int MOE_PLAN_WORDS = MOE_PLAN_SLOTS + MOE_PLAN_MAX * MOE_BATCH;
+struct MoePlanView {
+    const int32_t *plan = nullptr;
+    int k = 0;    // slots per token
+    int ffn = 0;  // activation row length
+};
+
 // int8 codes, group 64 or 128, at least GEMM_MIN_TOKENS tokens.
 bool gemm_supported(const marin_quant_matrix *w, size_t tokens);
 // y = the product of the quantized matrix with `tokens` activation rows (the same input and output modes as the
 // decode product); uses the context's workspace for the activation limbs.
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
+// Workspace bytes of launch_moe_gate_up (activation limbs of `tokens` rows of `cols`).
+size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group);
+// The grouped gate_up of a decode batch (2..MOE_BATCH tokens): every distinct selected expert's [2F][H] rows read
+// once for all tokens; act[t][slot][F] = SiLU(gate) * up for the tokens that selected it. `gate_up` is the stacked
+// [experts * 2F][H] matrix; `plan` as above, for at most `max_experts` distinct experts.
+void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *gate_up, const GemvIn &in, size_t tokens,
+                        const int32_t *plan, size_t max_experts, size_t k, size_t ffn, float *act);
 // Any token count: the GEMM when it applies, else the decode product GEMV_TOKENS tokens at a time.
 void launch_product(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
 

@@ -19,6 +19,7 @@
 #include <cstring>
 #include <vector>
 
+#include "gemm.hpp"
 #include "gemv.hpp"
 
 namespace marin {
@@ -107,6 +108,33 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route(const float *__restri
             weights[(size_t)b * k + j] = renorm ? sel_p[j] / s : sel_p[j];
         }
     }
+}
+
+// The routing plan of a decode batch (tokens * k <= 64 selections), one wave: the distinct selected experts in
+// ascending order and, per (distinct expert, token), the slot that selected it or -1 (layout in gemm.hpp).
+__global__ __launch_bounds__(64) void moe_plan(const int32_t *__restrict__ ids, int tokens, int k,
+                                               int32_t *__restrict__ plan) {
+    __shared__ int32_t slots[MOE_PLAN_MAX * MOE_BATCH];
+    const int lane = threadIdx.x, n = tokens * k;
+    const int id = ids[min(lane, n - 1)];
+    bool first = lane < n;  // first occurrence of its expert
+    int rank = 0;           // distinct experts below it
+    for (int j = 0; j < n; ++j) {
+        const int v = __shfl(id, j);
+        first = first && !(j < lane && v == id);
+    }
+    const unsigned long long firsts = __ballot(first);
+    for (int j = 0; j < n; ++j) {
+        const int v = __shfl(id, j);
+        rank += ((firsts >> j) & 1ull) && v < id;
+    }
+    for (int i = lane; i < MOE_PLAN_MAX * MOE_BATCH; i += 64) slots[i] = -1;
+    __syncthreads();
+    if (lane < n) slots[rank * MOE_BATCH + lane / k] = lane % k;
+    __syncthreads();
+    for (int i = lane; i < MOE_PLAN_MAX * MOE_BATCH; i += 64) plan[MOE_PLAN_SLOTS + i] = slots[i];
+    if (first) plan[MOE_PLAN_EXPERTS + rank] = id;
+    if (lane == 0) plan[0] = __popcll(firsts);
 }
 
 // grid: (H / 16 output tiles, tokens); a wave per expert slot j < k. WG: 64-column windows per group; MW: windows of
@@ -279,9 +307,33 @@ static void check_moe(const MoeArgs &a) {
 
 // One or more tokens' MoE FFN: out[t] += sum_j w[t][j] down_{e}(silu(gate_e x) * up_e x), x = RMSNorm(x[t]) when a
 // norm is given.
+// Device scratch of a grouped batch: the gate_up's activation limbs, then the plan.
+static size_t moe_scratch_bytes(const MoeArgs &a) {
+    return (moe_gate_up_workspace(a.tokens, a.hidden, a.gate_up->group) + 255) / 256 * 256 + MOE_PLAN_WORDS * 4;
+}
+
+static bool moe_grouped(const MoeArgs &a) { return a.tokens >= 2 && a.tokens <= (size_t)MOE_BATCH; }
+
 static void launch_moe(marin_gpu *g, const MoeArgs &a, int part = 0) {
     check_moe(a);
-    for (size_t t = 0; t < a.tokens && part != 2; ++t) {
+    if (moe_grouped(a) && part != 2) {
+        // a decode batch: every distinct selected expert's gate_up rows read once for all tokens
+        uint8_t *ws = (uint8_t *)g->workspace(moe_scratch_bytes(a));
+        int32_t *plan = (int32_t *)(ws + moe_scratch_bytes(a) - MOE_PLAN_WORDS * 4);
+        moe_plan<<<1, 64, 0, g->stream>>>(a.ids, (int)a.tokens, (int)a.k, plan);
+        g->launched();
+        GemvIn in;
+        in.mode = a.norm ? IN_NORM : IN_F32;
+        in.x = a.x;
+        in.x_stride = a.hidden;
+        in.norm = a.norm;
+        in.eps = a.eps;
+        launch_moe_gate_up(g, a.gate_up, in, a.tokens, plan, std::min(a.tokens * a.k, a.experts), a.k, a.ffn, a.act);
+        const double rows = (double)std::min(a.tokens * a.k, a.experts) * 2 * a.ffn;  // at most, once each
+        g->launched(marin_gpu::GEMV, rows * a.hidden + rows * (a.hidden / a.gate_up->group) * (a.gate_up->bf16_scales ? 2 : 4),
+                    "gemm_q8 (experts)");
+    }
+    for (size_t t = 0; t < a.tokens && part != 2 && !moe_grouped(a); ++t) {
         GemvIn in;
         in.mode = a.norm ? IN_NORM : IN_F32;
         in.x = a.x + t * a.hidden;
@@ -392,6 +444,10 @@ marin_status marin_moe_stack_time(marin_gpu *g, size_t layers, const marin_quant
             a.out = (float *)f32_of(out, tokens * a.hidden, "output");
             check_moe(a);
         }
+        // scratch grown before capture (a capture may not allocate)
+        size_t scratch = 0;
+        for (auto &a : per) scratch = std::max(scratch, moe_grouped(a) ? moe_scratch_bytes(a) : 0);
+        if (scratch) g->workspace(scratch);
         const char *ng = getenv("MARIN_NO_GRAPH");
         if (ng && *ng && *ng != '0') {
             // eager launches (for tracers that do not follow graph replays)

@@ -81,8 +81,11 @@ def stack_experts(experts, hidden, ffn, group, seed):
     return (np.concatenate(gate_up_c), np.concatenate(gate_up_s), np.concatenate(down_c), np.concatenate(down_s), deq)
 
 
+# tokens 1: the one-token product with a tile map; 2..8: the grouped batch (each distinct expert read once for all
+# tokens; experts 8 with k 8 makes every token share every expert); 9: one product per token
 @pytest.mark.parametrize("tokens,experts,k,hidden,ffn,group", [(1, 16, 4, 512, 256, 128), (3, 8, 8, 256, 768, 128),
-                                                                (2, 12, 2, 384, 128, 64)])
+                                                                (2, 12, 2, 384, 128, 64), (8, 16, 4, 256, 256, 128),
+                                                                (9, 6, 3, 256, 128, 128)])
 def test_expert_ffn_matches_the_dequantized_experts(gpu, tokens, experts, k, hidden, ffn, group):
     gu_c, gu_s, dn_c, dn_s, deq = stack_experts(experts, hidden, ffn, group, seed=11)
     gate_up = gpu.upload_quantized(experts * 2 * ffn, hidden, 8, group, gu_c, gu_s)
