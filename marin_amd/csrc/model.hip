@@ -29,7 +29,10 @@ using namespace marin;
 
 namespace marin {
 
-constexpr size_t CHUNK = 64;  // tokens per prompt pass through the layers (the products run as GEMMs)
+#ifndef MARIN_PREFILL_CHUNK
+#define MARIN_PREFILL_CHUNK 128
+#endif
+constexpr size_t CHUNK = MARIN_PREFILL_CHUNK;  // tokens per prompt pass through the layers (the products run as GEMMs)
 
 // One decode step's bookkeeping, after the output head left the greedy choice in *best as (total-order key, ~id)
 // (sampler/src/lib.rs:40-48: largest logit, lowest id on ties): record the token, clear the choice for the next

@@ -87,6 +87,25 @@ def test_synthetic_greedy_tokens_match_the_golden(gpu, name, monkeypatch):
         logits = model.forward([g["tokens"][s]], cache)
 
 
+def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu):
+    """A 300-token prompt runs as passes of at most the library's prompt chunk (128 tokens: 128, 128, 44), each
+    seeing the keys of the ones before; the greedy continuation and its top logits match the oracle's prompt pass."""
+    g = golden("mini")
+    shape = g["shape"]
+    prompt = o.synth_prompt(g["seed"] + 7, 300, shape["vocab"]).tolist()
+    steps = 6
+    toks, gaps, top_ids, top_vals = o.synth_greedy(shape, g["seed"], prompt, steps, with_top=True)
+    model = Qwen3(gpu, shape, seed=g["seed"])
+    cache = model.new_cache(len(prompt) + steps + 1)
+    logits = model.forward(prompt, cache)
+    for s in range(steps):
+        vals = np.asarray(top_vals[s], np.float64)
+        assert np.abs(logits[top_ids[s]] - vals).max() <= 1e-3 * (1 + np.abs(vals).max()), s
+        if gaps[s] > 1e-3:
+            assert o.argmax(logits) == toks[s], s
+        logits = model.forward([int(toks[s])], cache)
+
+
 def test_one_token_pass_equals_a_prompt_pass_and_runs_repeat(gpu):  # model/tests/quantized.rs:74-97
     g = golden("mini")
     model = Qwen3(gpu, g["shape"], seed=g["seed"])
