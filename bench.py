@@ -153,6 +153,54 @@ def bench_moe(m, args) -> int:
     return 0
 
 
+def bench_batch(m, args) -> int:
+    """Config 3 at batch N: N sequences, each with its own `--prompt`-token prompt of uniform random ids prefilled
+    through its own cache, then decoded together (one greedy token per sequence per step: every product over the N
+    tokens, one attention launch over all sequences, the step replayed as a HIP graph). value = N x K / wall seconds
+    of K timed steps."""
+    from marin_amd.qwen3 import SHAPES, Qwen3
+
+    shape = SHAPES["qwen3-8b"]
+    fmt = {"f32": m.KvFormat.F32, "f16": m.KvFormat.F16, "bf16": m.KvFormat.BF16}[args.kv]
+    B = args.batch
+    print(f"[bench] qwen3-8b int8 g128 batch {B}, prompt {args.prompt}, kv {args.kv}, warmup {args.warmup}, steps "
+          f"{args.steps}", file=sys.stderr, flush=True)
+    gpu = m.Gpu()
+    model = Qwen3(gpu, shape, seed=args.seed)
+    batch = model.new_batch(B, args.prompt + args.warmup + args.steps + 8, fmt)
+    rng = np.random.default_rng(args.seed)
+    t = time.perf_counter()
+    for i in range(B):
+        batch.prefill(i, rng.integers(0, shape["vocab"], args.prompt, dtype=np.uint32))
+    gpu.synchronize()
+    prefill_s = time.perf_counter() - t
+    print(f"[bench] {B} prompts in {prefill_s:.2f}s", file=sys.stderr, flush=True)
+    batch.decode(args.warmup)
+    gpu.synchronize()
+    t = time.perf_counter()
+    toks = batch.decode(args.steps)  # ends with a blocking download of the chosen ids
+    gpu.synchronize()
+    wall = time.perf_counter() - t
+    tok_s = B * args.steps / wall
+    print(f"[bench] batch {B}: {args.steps} steps in {wall * 1e3:.1f} ms: {tok_s:.1f} tok/s aggregate, "
+          f"{wall / args.steps * 1e3:.3f} ms per step", file=sys.stderr, flush=True)
+    line = {
+        "metric": f"decode tok/s Qwen3-8B-shape int8 bs={B} (aggregate over the batch)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (random-init N(0,0.02) weights quantized int8 g128 on device; uniform random prompt ids)",
+        "config": {"workload": f"qwen3-8b int8-g128 greedy decode, batch {B}, each sequence after a "
+                               f"{args.prompt}-token prompt", "prompt": args.prompt, "batch": B, "kv_format": args.kv,
+                   "layers": shape["layers"], "hidden": shape["hidden"], "ffn": shape["ffn"], "vocab": shape["vocab"]},
+        "weight_GBps": round(7.8046e9 / (wall / args.steps) / 1e9, 1),
+        "prefill_tok_s": round(B * args.prompt / prefill_s, 1),
+        "first_tokens": toks[:, :4].tolist(),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +216,9 @@ def main() -> int:
                          "dispatches); mean launch durations then come from the profiled steps' events")
     ap.add_argument("--probe-copy", type=float, default=0.0, metavar="MB",
                     help="only run the bandwidth probe: copies of MB megabytes (for counter calibration), then exit")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="config 3 at batch N (2..8): N sequences of the prompt length decoded together; one JSON line "
+                         "with the aggregate tok/s")
     ap.add_argument("--moe", action="store_true",
                     help="config 4 instead: the Qwen3-30B-A3B-shaped expert FFN stack at batch 1 and 8 (grouped-expert "
                          "GEMV GB/s), one JSON line")
@@ -193,6 +244,8 @@ def main() -> int:
 
     if args.moe:
         return bench_moe(m, args)
+    if args.batch > 1:
+        return bench_batch(m, args)
 
     shape = SHAPES["qwen3-8b"]
     fmt = {"f32": m.KvFormat.F32, "f16": m.KvFormat.F16, "bf16": m.KvFormat.BF16}[args.kv]

@@ -234,6 +234,20 @@ marin_status marin_qwen3_forward(marin_qwen3 *m, marin_qwen3_cache *c, const uin
 marin_status marin_qwen3_generate(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *prompt, size_t n,
                                   size_t steps, uint32_t *tokens_out);
 
+/* Extension (config 3 at batch 8; the reference decodes one sequence at a time): a decode batch of `batch` (1..8)
+ * sequences, each with its own KV cache of `capacity` positions. Prompts go in one sequence at a time; decoding then
+ * advances every sequence by one greedy token per step with each product over the whole batch (its weights read
+ * once per step) and one attention launch over all sequences. */
+typedef struct marin_qwen3_batch marin_qwen3_batch;
+marin_status marin_qwen3_batch_new(marin_qwen3 *m, size_t batch, size_t capacity, marin_kv_format format,
+                                   marin_qwen3_batch **out);
+void marin_qwen3_batch_free(marin_qwen3_batch *b);
+size_t marin_qwen3_batch_len(const marin_qwen3_batch *b, size_t seq);
+/* The prompt of sequence `seq` (a forward pass through its cache); its greedy choice is the sequence's next token. */
+marin_status marin_qwen3_batch_prefill(marin_qwen3_batch *b, size_t seq, const uint32_t *ids, size_t n);
+/* `steps` greedy tokens for every sequence (each must have had its prompt); tokens_out is [batch][steps]. */
+marin_status marin_qwen3_batch_decode(marin_qwen3_batch *b, size_t steps, uint32_t *tokens_out);
+
 /* Extension: continues greedy decoding for `steps` more tokens after a forward/generate on this cache (the
  * choice from the last pass's logits is the first token written). */
 marin_status marin_qwen3_decode(marin_qwen3 *m, marin_qwen3_cache *c, size_t steps, uint32_t *tokens_out);

@@ -116,6 +116,11 @@ SIGNATURES = {
     "marin_qwen3_forward": (st, [P, P, P, sz, P]),
     "marin_qwen3_generate": (st, [P, P, P, sz, sz, P]),
     "marin_qwen3_decode": (st, [P, P, sz, P]),
+    "marin_qwen3_batch_new": (st, [P, sz, sz, C.c_int, PP]),
+    "marin_qwen3_batch_free": (None, [P]),
+    "marin_qwen3_batch_len": (sz, [P, sz]),
+    "marin_qwen3_batch_prefill": (st, [P, sz, P, sz]),
+    "marin_qwen3_batch_decode": (st, [P, sz, P]),
     "marin_qwen3_profile_step": (st, [P, P, C.POINTER(StepProfileC)]),
     "marin_probe_copy": (st, [P, sz, C.c_int, C.POINTER(C.c_double)]),
     "marin_moe_route": (st, [P, P, sz, sz, sz, C.c_int, P, P]),

@@ -655,17 +655,19 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     // new position, the raw new key and value), issued first so they are not queued behind other workgroups' rows,
     // then the page addresses
     constexpr int QPW = (R + NW - 1) / NW;  // q heads per wave
+    // with FUSE, sequence b's q | k | v row (one token each) is row b of the fused rows
+    const float *fq = FUSE ? fuse.qkv + (size_t)b * (heads + 2 * kv_heads) * hd : nullptr;
     HeadIn qin[QPW], kin;
     float vin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (FUSE) {
 #pragma unroll
         for (int j = 0; j < QPW; ++j) {
             const int r = wave + j * NW;
-            if (r < group) qin[j] = load_head(fuse.qkv + (size_t)(kvh * group + r) * hd, fuse.q_norm, fuse.freq, hd, lane);
+            if (r < group) qin[j] = load_head(fq + (size_t)(kvh * group + r) * hd, fuse.q_norm, fuse.freq, hd, lane);
         }
         if (owns_new && wave == NW - 1) {
-            kin = load_head(fuse.qkv + (size_t)(heads + kvh) * hd, fuse.k_norm, fuse.freq, hd, lane);
-            const float *vsrc = fuse.qkv + (size_t)(heads + kv_heads + kvh) * hd;
+            kin = load_head(fq + (size_t)(heads + kvh) * hd, fuse.k_norm, fuse.freq, hd, lane);
+            const float *vsrc = fq + (size_t)(heads + kv_heads + kvh) * hd;
 #pragma unroll
             for (int k = 0; k < 4; ++k) vin[k] = lane + 64 * k < hd ? vsrc[lane + 64 * k] : 0.0f;
         }
@@ -1204,6 +1206,8 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
         }
         return;
     }
+    // the fused inputs of attention_split are one sequence's token rows
+    if (a.fuse.qkv && a.batch > 1) unsupported("fused attention over a batch (one-token decode only)", 1, a.batch);
     if (g->only && strcmp(g->only, "attention_split")) return;
     dim3 grid((unsigned)splits, (unsigned)(a.kv_heads * row_groups), (unsigned)a.batch);
     switch (a.geom.format) {

@@ -32,6 +32,13 @@ constexpr int GM_TOKENS = 32;     // tokens per workgroup of the prompt GEMM
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
+// (f32 total order, lowest row on ties) as one word: the larger word is the greedy choice (sampler/src/lib.rs:40-48)
+__device__ __forceinline__ unsigned long long choice_key(float v, int row) {
+    const int b = __float_as_int(v);
+    const unsigned k = (unsigned)(b ^ (int)(((unsigned)(b >> 31)) >> 1)) ^ 0x80000000u;
+    return (unsigned long long)k << 32 | (unsigned long long)(0xffffffffu - (unsigned)row);
+}
+
 }  // namespace
 
 // One token row per workgroup. GCOLS = quantization group width (a multiple of 4, at most 4 * 64).
@@ -138,6 +145,8 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
     // B fragments of one group: [buffer][window][token tile][64 lanes] x 16 bytes, and the tokens' group factors
     __shared__ u32x4 bl[2][WG][TT][64];
     __shared__ float ex[2][TOK];
+    __shared__ unsigned long long best_s[TOK];  // per-token greedy choice of the block (argmax_each)
+    if (threadIdx.x < TOK) best_s[threadIdx.x] = 0ull;  // read after the pipeline's barriers
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q = lane >> 4;
@@ -284,11 +293,30 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
                 v[k] = x;
             }
             const int tok = t0 + 4 * j + c / 4;
-            if ((c & 3) != 0 || tok >= tokens || tile >= tiles) continue;
-            const float r = rsv[tok];
+            const int row0 = tile * 16 + 4 * q;
+            const bool mine = (c & 3) == 0 && tok < tokens && tile < tiles;
+            const float r = rsv[min(tok, tokens - 1)];
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[k] *= r;
-            const int row0 = tile * 16 + 4 * q;
+            if constexpr (!MOE) {
+                if (out.argmax_each) {
+                    // the rows of lanes q = 0..3 (same token) reduced by shuffles, then one LDS max per token
+                    unsigned long long key = 0ull;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (mine && row0 + k < rows) {
+                            const unsigned long long kk = choice_key(v[k], row0 + k);
+                            key = kk > key ? kk : key;
+                        }
+#pragma unroll
+                    for (int o = 16; o < 64; o <<= 1) {
+                        const unsigned long long other = __shfl_xor(key, o);
+                        key = other > key ? other : key;
+                    }
+                    if (mine && q == 0 && key) atomicMax(&best_s[tok - t0], key);
+                }
+            }
+            if (!mine) continue;
             if constexpr (MOE) {
                 // the token's slot for this expert (-1: it did not select it); rows are the expert's interleaved
                 // gate/up pairs
@@ -324,27 +352,46 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
             }
         }
     }
+    if constexpr (!MOE) {
+        if (out.argmax_each) {
+            __syncthreads();
+            if ((int)threadIdx.x < TOK && t0 + (int)threadIdx.x < tokens && best_s[threadIdx.x])
+                atomicMax(out.argmax + t0 + threadIdx.x, best_s[threadIdx.x]);
+        }
+    }
+}
+
+bool gemm_layout_ok(const marin_quant_matrix *w) {
+    return w->bits == 8 && w->windowed && (w->group == 64 || w->group == 128) && w->cols % w->group == 0;
 }
 
 bool gemm_supported(const marin_quant_matrix *w, size_t tokens) {
-    return tokens >= GEMM_MIN_TOKENS && w->bits == 8 && w->windowed && (w->group == 64 || w->group == 128) &&
-           w->cols % w->group == 0;
+    return tokens >= GEMM_MIN_TOKENS && gemm_layout_ok(w);
+}
+
+template <int WG, typename ST, int TOK>
+static void launch_tok(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
+                       const float *rs, const GemvOut &out, size_t tokens) {
+    const int tiles = (int)(w->rows_padded / 16);
+    const int rows_per_block = GM_WAVES * GM_ROW_TILES * 16;
+    dim3 grid((unsigned)((w->rows_padded + rows_per_block - 1) / rows_per_block), (unsigned)((tokens + TOK - 1) / TOK));
+    gemm_q8<WG, ST, TOK, false><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(
+        w->codes, (const ST *)w->scales, limbs, exps, rs, out, (int)tokens, (int)w->rows, (int)w->cols, tiles,
+        MoePlanView{});
 }
 
 template <int WG, typename ST>
 static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
                      const float *rs, const GemvOut &out, size_t tokens) {
-    const int tiles = (int)(w->rows_padded / 16);
-    const int rows_per_block = GM_WAVES * GM_ROW_TILES * 16;
-    dim3 grid((unsigned)((w->rows_padded + rows_per_block - 1) / rows_per_block),
-              (unsigned)((tokens + GM_TOKENS - 1) / GM_TOKENS));
-    gemm_q8<WG, ST, GM_TOKENS, false><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(
-        w->codes, (const ST *)w->scales, limbs, exps, rs, out, (int)tokens, (int)w->rows, (int)w->cols, tiles,
-        MoePlanView{});
+    // a decode batch in one token block of 8; prompts in blocks of 32
+    if (tokens <= (size_t)MOE_BATCH) launch_tok<WG, ST, MOE_BATCH>(g, w, limbs, exps, rs, out, tokens);
+    else launch_tok<WG, ST, GM_TOKENS>(g, w, limbs, exps, rs, out, tokens);
 }
 
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
-    if (!gemm_supported(w, tokens)) unsupported("matrix-core GEMM layout (int8, group 64 or 128)", 128, w->group);
+    if (!tokens) return;
+    if (!gemm_layout_ok(w)) unsupported("matrix-core GEMM layout (int8, group 64 or 128)", 128, w->group);
+    if (out.argmax && !out.argmax_each) unsupported("GEMM greedy choice (one per token only)", 1, 0);
     const size_t cols = w->cols, groups = w->groups();
     // workspace: limbs [tokens][4][cols] | exps [tokens][groups] | rs [tokens]
     const size_t limb_bytes = (tokens * 4 * cols + 15) / 16 * 16;
@@ -421,7 +468,7 @@ void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *w, const GemvIn 
 
 void launch_product(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     if (!tokens) return;
-    if (gemm_supported(w, tokens) && !out.argmax) {
+    if ((gemm_supported(w, tokens) && !out.argmax) || (out.argmax_each && gemm_layout_ok(w))) {
         launch_gemm(g, w, in, out, tokens);
         return;
     }

@@ -5,7 +5,7 @@
 
 namespace marin {
 
-constexpr size_t GEMM_MIN_TOKENS = 16;  // token counts from which the GEMM replaces chunks of the decode product
+constexpr size_t GEMM_MIN_TOKENS = 5;  // token counts from which the GEMM replaces chunks of the decode product
 
 // The routing plan of a decode batch's MoE layer (device int32 words, written by moe_plan): [0] the count U of
 // distinct selected experts; [MOE_PLAN_EXPERTS + u] the u-th smallest of them; [MOE_PLAN_SLOTS + u * MOE_BATCH + t]
@@ -23,8 +23,11 @@ struct MoePlanView {
 
 // int8 codes, group 64 or 128, at least GEMM_MIN_TOKENS tokens.
 bool gemm_supported(const marin_quant_matrix *w, size_t tokens);
-// y = the product of the quantized matrix with `tokens` activation rows (the same input and output modes as the
-// decode product); uses the context's workspace for the activation limbs.
+// The GEMM's layout requirement alone (int8 codes, group 64 or 128).
+bool gemm_layout_ok(const marin_quant_matrix *w);
+// y = the product of the quantized matrix with `tokens` (>= 1) activation rows (the same input and output modes as
+// the decode product; with out.argmax_each, the greedy choice of every token into out.argmax[t]); uses the
+// context's workspace for the activation limbs. Token blocks of 8 for up to 8 tokens, of 32 beyond.
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
 // Workspace bytes of launch_moe_gate_up (activation limbs of `tokens` rows of `cols`).
 size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group);

@@ -37,6 +37,7 @@ struct GemvOut {
     void *y = nullptr;
     size_t y_stride = 0;
     unsigned long long *argmax = nullptr;  // optional: atomic max of (total-order key, ~row) of the last token
+    bool argmax_each = false;              // with argmax: one word per token, argmax[t] (multi-token GEMM only)
 };
 
 bool gemv_supported(const marin_quant_matrix *w);

@@ -78,6 +78,34 @@ __global__ void embed_device_ids(const uint8_t *__restrict__ codes, const float 
             (float)(int8_t)codes[code_offset(row, i, cols, true, 16)] * srow[(i / group) * 16];
 }
 
+// A decode batch's bookkeeping (one workgroup per sequence b): the greedy choice best[b] of the last pass becomes
+// the sequence's token (recorded at tokens_out[step * batch + b]), the choice is cleared, the sequence's position
+// advances (pos[b] += 1, ctx[b] = pos[b] + 1, step[b] += 1) and the token's table row is embedded into hidden[b].
+// state: pos [batch] | ctx [batch] | step [batch].
+__global__ __launch_bounds__(512) void advance_batch(unsigned long long *best, uint32_t *tokens_out, uint32_t *state,
+                                                     int batch, const uint8_t *__restrict__ codes,
+                                                     const float *__restrict__ scales, float *__restrict__ hidden,
+                                                     int cols, int group) {
+    __shared__ uint32_t id_s;
+    const int b = blockIdx.x;
+    if (threadIdx.x == 0) {
+        const uint32_t id = 0xffffffffu - (uint32_t)(best[b] & 0xffffffffull);
+        best[b] = 0ull;
+        tokens_out[(size_t)state[2 * batch + b] * batch + b] = id;
+        state[b] += 1;
+        state[batch + b] = state[b] + 1;
+        state[2 * batch + b] += 1;
+        id_s = id;
+    }
+    __syncthreads();
+    const size_t row = id_s;
+    const int groups = cols / group;
+    const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
+    float *h = hidden + (size_t)b * cols;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x)
+        h[i] = (float)(int8_t)codes[code_offset(row, i, cols, true, 16)] * srow[(i / group) * 16];
+}
+
 }  // namespace marin
 
 struct Layer {
@@ -110,6 +138,28 @@ struct marin_qwen3_cache {
     uint32_t *attn_counters = nullptr;
     hipGraphExec_t graph = nullptr;
     size_t graph_capacity_ctx = 0;
+};
+
+// A decode batch: `seqs` sequences, each with its own KV cache (prefilled one at a time through its own cache),
+// decoded together: one token per sequence per step, every product over the whole batch (weights read once), one
+// attention launch over all sequences through a combined page-address table.
+struct marin_qwen3_batch {
+    marin_qwen3 *model = nullptr;
+    std::vector<marin_qwen3_cache *> seqs;
+    float *hidden = nullptr, *qkv = nullptr, *ctx = nullptr, *act = nullptr, *logits = nullptr;
+    unsigned long long *best = nullptr;  // [batch] greedy choices
+    uint32_t *state = nullptr;           // pos [batch] | ctx [batch] | step [batch]
+    uint64_t *tables = nullptr;          // [batch][table_stride] page addresses
+    size_t table_stride = 0;
+    std::vector<uint64_t> host_tables;
+    uint32_t *tokens_out = nullptr;  // [steps][batch]
+    size_t tokens_cap = 0;           // steps
+    float *partials = nullptr;
+    size_t partial_floats = 0;
+    uint32_t *counters = nullptr;
+    size_t counter_count = 0;
+    size_t capacity = 0;
+    hipGraphExec_t graph = nullptr;
 };
 
 static void check_config(const marin_qwen3_config *c) {
@@ -201,87 +251,115 @@ static void free_cache_graph(marin_qwen3_cache *c) {
     }
 }
 
-// One pass over `n` (<= CHUNK) tokens at the position in c->state, whose embeddings are already in c->hidden. Writes
-// the last token's logits and its greedy choice. `max_ctx` bounds the context for the attention grid; `host_ctx`
-// (when known) only feeds launch accounting.
-static void pass(marin_qwen3 *m, marin_qwen3_cache *c, size_t n, size_t max_ctx, size_t host_ctx = 0,
-                 bool head_out = true) {
+// What a pass reads and writes: `batch` sequences of `tokens` tokens each (rows batch * tokens, sequence-major),
+// their embeddings in `hidden`; attention through `tables` (sequence b's page addresses at b * table_stride) with
+// the sequences' context lengths in `ctx_lens`.
+struct PassIo {
+    float *hidden, *qkv, *ctx, *act, *logits;
+    unsigned long long *best;
+    const uint64_t *tables;
+    size_t table_stride;
+    const uint32_t *ctx_lens;
+    size_t batch, tokens;
+    const marin_kv *kv;  // geometry and format (shared by every sequence)
+    float *partials;
+    size_t partial_floats;
+    uint32_t *counters;
+    size_t counter_count;
+};
+
+static PassIo io_of(marin_qwen3_cache *c, size_t n) {
+    return PassIo{c->hidden, c->qkv, c->ctx, c->act, c->logits, c->best, c->kv->page_ptrs, 0, c->state + 1, 1, n,
+                  c->kv, c->attn_partials, c->attn_partial_floats, c->attn_counters,
+                  attention_counters(1, CHUNK, c->model->cfg.heads)};
+}
+
+// One pass at the positions in the device state, whose embeddings are already in io.hidden. With one sequence,
+// writes the last token's logits and greedy choice; with a batch (one token per sequence), every sequence's logits
+// and greedy choice (best[b]). `max_ctx` bounds the context for the attention grid; `host_ctx` (when known) only
+// feeds launch accounting.
+static void pass(marin_qwen3 *m, const PassIo &io, size_t max_ctx, size_t host_ctx = 0, bool head_out = true) {
     marin_gpu *g = m->gpu;
     const auto &cfg = m->cfg;
     const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd(), F = cfg.ffn;
+    const size_t n = io.batch * io.tokens;  // rows of every product
     for (size_t l = 0; l < m->layers.size(); ++l) {
         Layer &L = m->layers[l];
         GemvIn norm_in;
         norm_in.mode = IN_NORM;
-        norm_in.x = c->hidden;
+        norm_in.x = io.hidden;
         norm_in.x_stride = H;
         norm_in.norm = L.input_norm;
         norm_in.eps = cfg.rms_eps;
         GemvOut qkv_out;
         qkv_out.mode = OUT_F32;
-        qkv_out.y = c->qkv;
+        qkv_out.y = io.qkv;
         qkv_out.y_stride = qd + 2 * kvd;
         launch_product(g, L.qkv, norm_in, qkv_out, n);
-        const KvGeom geom = c->kv->geom(l);
         AttentionArgs a{};
         a.q = nullptr;
         a.bf16_io = false;
-        a.out = c->ctx;
-        a.fuse.qkv = c->qkv;
+        a.out = io.ctx;
+        a.fuse.qkv = io.qkv;
         a.fuse.q_norm = L.q_norm;
         a.fuse.k_norm = L.k_norm;
         a.fuse.freq = m->freq;
         a.fuse.eps = cfg.rms_eps;
-        a.tables = c->kv->page_ptrs;
-        a.table_stride = 0;
-        a.ctx = c->state + 1;
-        a.batch = 1;
-        a.tokens = n;
+        a.tables = io.tables;
+        a.table_stride = io.table_stride;
+        a.ctx = io.ctx_lens;
+        a.batch = io.batch;
+        a.tokens = io.tokens;
         a.heads = cfg.heads;
         a.kv_heads = cfg.kv_heads;
-        a.geom = geom;
+        a.geom = io.kv->geom(l);
         a.max_ctx = max_ctx;
-        a.partials = c->attn_partials;
-        a.partial_floats = c->attn_partial_floats;
-        a.counters = c->attn_counters;
-        a.counter_count = attention_counters(1, CHUNK, cfg.heads);
-        a.bytes_hint = (double)host_ctx * 2 * kvd * kv_elem_bytes(c->kv->format) + 2.0 * n * qd * 4;
+        a.partials = io.partials;
+        a.partial_floats = io.partial_floats;
+        a.counters = io.counters;
+        a.counter_count = io.counter_count;
+        a.bytes_hint = (double)io.batch * host_ctx * 2 * kvd * kv_elem_bytes(io.kv->format) + 2.0 * n * qd * 4;
         launch_attention(g, a);
         GemvIn ctx_in;
         ctx_in.mode = IN_F32;
-        ctx_in.x = c->ctx;
+        ctx_in.x = io.ctx;
         ctx_in.x_stride = qd;
         GemvOut add_out;
         add_out.mode = OUT_ADD;
-        add_out.y = c->hidden;
+        add_out.y = io.hidden;
         add_out.y_stride = H;
         launch_product(g, L.o, ctx_in, add_out, n);
         GemvIn post_in = norm_in;
         post_in.norm = L.post_norm;
         GemvOut silu_out;
         silu_out.mode = OUT_SILU;
-        silu_out.y = c->act;
+        silu_out.y = io.act;
         silu_out.y_stride = F;
         launch_product(g, L.gate_up, post_in, silu_out, n);
         GemvIn act_in;
         act_in.mode = IN_F32;
-        act_in.x = c->act;
+        act_in.x = io.act;
         act_in.x_stride = F;
         launch_product(g, L.down, act_in, add_out, n);
     }
     if (!head_out) return;  // a prompt's earlier chunks need no logits
     GemvIn last;
     last.mode = IN_NORM;
-    last.x = c->hidden + (n - 1) * H;
+    last.x = io.batch == 1 ? io.hidden + (n - 1) * H : io.hidden;
     last.x_stride = H;
     last.norm = m->final_norm;
     last.eps = cfg.rms_eps;
     GemvOut head;
     head.mode = OUT_F32;
-    head.y = c->logits;
+    head.y = io.logits;
     head.y_stride = cfg.vocab;
-    head.argmax = c->best;
-    launch_gemv(g, m->head(), last, head, 1);
+    head.argmax = io.best;
+    if (io.batch == 1) {
+        launch_gemv(g, m->head(), last, head, 1);
+    } else {
+        head.argmax_each = true;
+        launch_product(g, m->head(), last, head, io.batch);
+    }
 }
 
 static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n) {
@@ -301,7 +379,7 @@ static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids
         embed_device_ids<<<dim3((unsigned)nt), dim3(256), 0, g->stream>>>(
             m->embed->codes, (const float *)m->embed->scales, c->ids, c->hidden, (int)m->cfg.hidden, (int)m->cfg.group);
         g->launched();
-        pass(m, c, nt, start + t0 + nt, 0, t0 + nt == n);
+        pass(m, io_of(c, nt), start + t0 + nt, 0, t0 + nt == n);
         c->kv->len = start + t0 + nt;
     }
 }
@@ -451,7 +529,7 @@ static void decode_step(marin_qwen3 *m, marin_qwen3_cache *c, size_t host_ctx) {
                                       (const float *)m->embed->scales, c->hidden, (int)m->cfg.hidden,
                                       (int)m->cfg.group);
     g->launched();
-    pass(m, c, 1, c->kv->capacity, host_ctx);
+    pass(m, io_of(c, 1), c->kv->capacity, host_ctx);
 }
 
 static bool graphs_enabled() {
@@ -606,7 +684,7 @@ marin_status marin_qwen3_time_kernel(marin_qwen3 *m, marin_qwen3_cache *c, const
         HIP_CHECK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
         g->only = only.c_str();
         try {
-            pass(m, c, 1, c->kv->capacity, 0);
+            pass(m, io_of(c, 1), c->kv->capacity, 0);
         } catch (...) {
             g->only = nullptr;
             g->skipped = false;
@@ -646,6 +724,163 @@ marin_status marin_qwen3_profile_launches(marin_qwen3 *m, marin_qwen3_cache *c, 
         const auto recs = profile_launches(m, c);
         for (size_t i = 0; i < recs.size() && i < cap; ++i) out[i] = recs[i];
         *count = recs.size();
+    });
+}
+
+static void free_batch_graph(marin_qwen3_batch *b) {
+    if (b->graph) {
+        unregister_graph(b->graph);
+        (void)hipGraphExecDestroy(b->graph);
+        b->graph = nullptr;
+    }
+}
+
+static PassIo io_of(marin_qwen3_batch *b) {
+    return PassIo{b->hidden, b->qkv, b->ctx, b->act, b->logits, b->best, b->tables, b->table_stride,
+                  b->state + b->seqs.size(), b->seqs.size(), 1, b->seqs[0]->kv, b->partials, b->partial_floats,
+                  b->counters, b->counter_count};
+}
+
+// One batch decode step: every sequence's choice becomes its token, then one pass of the batch.
+static void batch_step(marin_qwen3 *m, marin_qwen3_batch *b) {
+    marin_gpu *g = m->gpu;
+    advance_batch<<<(unsigned)b->seqs.size(), 512, 0, g->stream>>>(
+        b->best, b->tokens_out, b->state, (int)b->seqs.size(), m->embed->codes, (const float *)m->embed->scales,
+        b->hidden, (int)m->cfg.hidden, (int)m->cfg.group);
+    g->launched();
+    pass(m, io_of(b), b->capacity, 0);
+}
+
+
+void marin_qwen3_batch_free(marin_qwen3_batch *b) {
+    if (!b) return;
+    marin_gpu *g = b->model->gpu;
+    (void)hipStreamSynchronize(g->stream);
+    free_batch_graph(b);
+    for (auto *c : b->seqs) marin_qwen3_cache_free(c);
+    for (void *p : {(void *)b->hidden, (void *)b->qkv, (void *)b->ctx, (void *)b->act, (void *)b->logits,
+                    (void *)b->best, (void *)b->state, (void *)b->tables, (void *)b->tokens_out, (void *)b->partials,
+                    (void *)b->counters})
+        g->release(p);
+    delete b;
+}
+
+marin_status marin_qwen3_batch_new(marin_qwen3 *m, size_t batch, size_t capacity, marin_kv_format format,
+                                   marin_qwen3_batch **out) {
+    return guard([&] {
+        if (batch < 1 || batch > MOE_BATCH) unsupported("decode batch (sequences)", MOE_BATCH, batch);
+        marin_gpu *g = m->gpu;
+        const auto &cfg = m->cfg;
+        auto b = std::make_unique<marin_qwen3_batch>();
+        b->model = m;
+        b->capacity = capacity;
+        try {
+            for (size_t i = 0; i < batch; ++i) {
+                marin_qwen3_cache *c = nullptr;
+                marin_status st = marin_qwen3_cache_new(m, capacity, format, &c);
+                if (st != MARIN_OK) throw Error(st, marin_last_error());
+                b->seqs.push_back(c);
+            }
+            const size_t H = cfg.hidden, qd = m->qd(), kvd = m->kvd();
+            b->hidden = (float *)g->alloc(batch * H * 4, true);
+            b->qkv = (float *)g->alloc(batch * (qd + 2 * kvd) * 4, true);
+            b->ctx = (float *)g->alloc(batch * qd * 4, true);
+            b->act = (float *)g->alloc(batch * cfg.ffn * 4, true);
+            b->logits = (float *)g->alloc(batch * cfg.vocab * 4, true);
+            b->best = (unsigned long long *)g->alloc(batch * 8, true);
+            b->state = (uint32_t *)g->alloc(3 * batch * 4, true);
+            b->table_stride = b->seqs[0]->kv->pool.limit;
+            b->tables = (uint64_t *)g->alloc(std::max<size_t>(batch * b->table_stride, 1) * 8, true);
+            b->host_tables.assign(batch * b->table_stride, 0);
+            b->partial_floats = attention_partial_floats(batch, 1, cfg.heads, cfg.head_dim, capacity, g->cu_count);
+            b->partials = (float *)g->alloc(b->partial_floats * 4, false);
+            b->counter_count = attention_counters(batch, 1, cfg.heads);
+            b->counters = (uint32_t *)g->alloc(b->counter_count * 4, true);
+        } catch (...) {
+            marin_qwen3_batch_free(b.release());
+            throw;
+        }
+        *out = b.release();
+    });
+}
+
+size_t marin_qwen3_batch_len(const marin_qwen3_batch *b, size_t seq) {
+    return seq < b->seqs.size() ? b->seqs[seq]->kv->len : 0;
+}
+
+marin_status marin_qwen3_batch_prefill(marin_qwen3_batch *b, size_t seq, const uint32_t *ids, size_t n) {
+    return guard([&] {
+        if (seq >= b->seqs.size()) shape("batch sequence", b->seqs.size(), seq);
+        marin_qwen3_cache *c = b->seqs[seq];
+        run_prompt(b->model, c, ids, n);
+        // the prompt's greedy choice is the sequence's first decoded token
+        HIP_CHECK(hipMemcpyAsync(b->best + seq, c->best, 8, hipMemcpyDeviceToDevice, b->model->gpu->stream));
+    });
+}
+
+// Greedy decoding of `steps` tokens for every sequence; tokens_out is [batch][steps].
+marin_status marin_qwen3_batch_decode(marin_qwen3_batch *b, size_t steps, uint32_t *tokens_out) {
+    return guard([&] {
+        marin_qwen3 *m = b->model;
+        marin_gpu *g = m->gpu;
+        const size_t B = b->seqs.size();
+        if (steps == 0) return;
+        std::vector<uint32_t> init(3 * B, 0u);
+        for (size_t i = 0; i < B; ++i) {
+            marin_kv *kv = b->seqs[i]->kv;
+            if (kv->len == 0) throw Error(MARIN_SHAPE, "every sequence of a batch needs its prompt first", 1, 0);
+            if (kv->len + steps > kv->capacity) shape("kv positions", kv->capacity, kv->len + steps);
+            kv->reserve(kv->len + steps);
+            std::copy(kv->host_ptrs.begin(), kv->host_ptrs.begin() + std::min(kv->host_ptrs.size(), b->table_stride),
+                      b->host_tables.begin() + i * b->table_stride);
+            init[i] = (uint32_t)(kv->len - 1);  // advanced to len by the first choice
+            init[B + i] = (uint32_t)kv->len;
+        }
+        g->upload(b->tables, b->host_tables.data(), b->host_tables.size() * 8);
+        g->upload(b->state, init.data(), init.size() * 4);
+        if (steps > b->tokens_cap) {
+            HIP_CHECK(hipStreamSynchronize(g->stream));
+            free_batch_graph(b);  // the graph holds the old tokens_out address
+            g->release(b->tokens_out);
+            b->tokens_out = nullptr;
+            b->tokens_out = (uint32_t *)g->alloc(steps * B * 4, false);
+            b->tokens_cap = steps;
+        }
+        // the products' activation limbs: grown before a capture (a capture may not allocate)
+        const auto &cfg = m->cfg;
+        g->workspace(moe_gate_up_workspace(B, std::max(std::max(cfg.hidden, cfg.ffn), m->qd()), cfg.group));
+        if (graphs_enabled()) {
+            if (!b->graph) {
+                hipGraph_t graph;
+                HIP_CHECK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
+                try {
+                    batch_step(m, b);
+                } catch (...) {
+                    hipGraph_t junk;
+                    (void)hipStreamEndCapture(g->stream, &junk);
+                    if (junk) (void)hipGraphDestroy(junk);
+                    throw;
+                }
+                HIP_CHECK(hipStreamEndCapture(g->stream, &graph));
+                hipError_t e = hipGraphInstantiate(&b->graph, graph, nullptr, nullptr, 0);
+                (void)hipGraphDestroy(graph);
+                hip_check(e, "hipGraphInstantiate");
+                register_graph(b->graph);
+            }
+            for (size_t s = 0; s < steps; ++s) {
+                HIP_CHECK(hipGraphLaunch(b->graph, g->stream));
+                g->traffic.launches++;
+            }
+        } else {
+            for (size_t s = 0; s < steps; ++s) batch_step(m, b);
+        }
+        for (auto *c : b->seqs) c->kv->len += steps;
+        if (tokens_out) {
+            std::vector<uint32_t> t(steps * B);
+            g->download(t.data(), b->tokens_out, t.size() * 4);
+            for (size_t s = 0; s < steps; ++s)
+                for (size_t i = 0; i < B; ++i) tokens_out[i * steps + s] = t[s * B + i];
+        }
     });
 }
 

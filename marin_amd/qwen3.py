@@ -132,6 +132,11 @@ class Qwen3:
     def new_cache(self, capacity: int, fmt: KvFormat = KvFormat.F32) -> "Qwen3Cache":
         return Qwen3Cache(self, capacity, fmt)
 
+    def new_batch(self, batch: int, capacity: int, fmt: KvFormat = KvFormat.F32) -> "Qwen3Batch":
+        """A decode batch of `batch` (1..8) sequences of `capacity` positions each (extension; see
+        include/marin_hip.h)."""
+        return Qwen3Batch(self, batch, capacity, fmt)
+
     def forward(self, tokens, cache: "Qwen3Cache") -> np.ndarray:
         ids = np.ascontiguousarray(tokens, np.uint32).ravel()
         logits = np.empty(self.shape["vocab"], np.float32)
@@ -194,6 +199,35 @@ class Qwen3Cache:
     def __del__(self):
         if getattr(self, "_h", None) and alive():
             lib.marin_qwen3_cache_free(self._h)
+            self._h = None
+
+
+class Qwen3Batch:
+    """Sequences decoded together: prompts one sequence at a time, then every sequence one greedy token per step."""
+
+    def __init__(self, model: Qwen3, batch: int, capacity: int, fmt: KvFormat):
+        h = C.c_void_p()
+        check(lib.marin_qwen3_batch_new(model._h, batch, capacity, int(fmt), C.byref(h)))
+        self._h = h
+        self._model = model
+        self.batch = batch
+
+    def length(self, seq: int) -> int:
+        return int(lib.marin_qwen3_batch_len(self._h, seq))
+
+    def prefill(self, seq: int, tokens) -> None:
+        ids = np.ascontiguousarray(tokens, np.uint32).ravel()
+        check(lib.marin_qwen3_batch_prefill(self._h, seq, ids.ctypes.data, ids.size))
+
+    def decode(self, steps: int) -> np.ndarray:
+        """[batch][steps] greedy tokens."""
+        out = np.zeros((self.batch, steps), np.uint32)
+        check(lib.marin_qwen3_batch_decode(self._h, steps, out.ctypes.data))
+        return out
+
+    def __del__(self):
+        if getattr(self, "_h", None) and alive():
+            lib.marin_qwen3_batch_free(self._h)
             self._h = None
 
 

@@ -106,6 +106,41 @@ def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu):
         logits = model.forward([int(toks[s])], cache)
 
 
+def agree_until_a_near_tie(got, exp, gaps, tie=1e-3):
+    """Greedy sequences agree, or first differ at a step whose oracle top-1/top-2 gap is below `tie`."""
+    for i, (a, b) in enumerate(zip(got, exp)):
+        if a != b:
+            assert gaps[i] < tie, (i, a, b, gaps[i])
+            return i
+    return len(exp)
+
+
+@pytest.mark.parametrize("batch", [3, 8])
+def test_batch_decode_matches_each_sequence_on_the_oracle(gpu, batch, monkeypatch):
+    """Sequences of different prompt lengths decoded together (every product over the batch, one attention launch
+    over all sequences) give each sequence the oracle's greedy tokens; graph replay and eager launches agree."""
+    g = golden("mini")
+    shape = g["shape"]
+    steps = 8
+    prompts = [o.synth_prompt(g["seed"] + 11 + i, 17 + 9 * i, shape["vocab"]).tolist() for i in range(batch)]
+    model = Qwen3(gpu, shape, seed=g["seed"])
+    runs = []
+    for graph in (True, False):
+        monkeypatch.setenv("MARIN_NO_GRAPH", "0" if graph else "1")
+        b = model.new_batch(batch, max(len(p) for p in prompts) + 2 * steps + 1)
+        for i, p in enumerate(prompts):
+            b.prefill(i, p)
+        first = b.decode(steps // 2)
+        runs.append(np.concatenate([first, b.decode(steps - steps // 2)], axis=1))
+        assert [b.length(i) for i in range(batch)] == [len(p) + steps for p in prompts]
+    assert (runs[0] == runs[1]).all()
+    compared = 0
+    for i, p in enumerate(prompts):
+        toks, gaps = o.synth_greedy(shape, g["seed"], p, steps)
+        compared += agree_until_a_near_tie(runs[0][i].tolist(), toks.tolist(), gaps)
+    assert compared >= batch * steps // 2
+
+
 def test_one_token_pass_equals_a_prompt_pass_and_runs_repeat(gpu):  # model/tests/quantized.rs:74-97
     g = golden("mini")
     model = Qwen3(gpu, g["shape"], seed=g["seed"])
