@@ -424,6 +424,18 @@ size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group) {
     return align16(tokens * 4 * cols) + align16(tokens * (cols / group) * 4) + tokens * 4;
 }
 
+ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group) {
+    const size_t limb_bytes = align16(tokens * 4 * cols), exp_bytes = align16(tokens * (cols / group) * 4);
+    uint8_t *ws = (uint8_t *)g->workspace(moe_gate_up_workspace(tokens, cols, group));
+    int8_t *limbs = (int8_t *)ws;
+    float *exps = (float *)(ws + limb_bytes);
+    float *rs = (float *)(ws + limb_bytes + exp_bytes);
+    if (group == 128) quantize_act<128><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    else quantize_act<64><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    g->launched();
+    return ActLimbs{limbs, exps, rs};
+}
+
 template <int WG, typename ST>
 static void launch_moe_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
                          const float *rs, size_t tokens, const MoePlanView &plan, size_t max_experts, float *act) {
@@ -468,6 +480,10 @@ void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *w, const GemvIn 
 
 void launch_product(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     if (!tokens) return;
+    if (gemv_batch_supported(w, tokens) && (!out.argmax || out.argmax_each)) {
+        launch_gemv_batch(g, w, in, out, tokens);
+        return;
+    }
     if ((gemm_supported(w, tokens) && !out.argmax) || (out.argmax_each && gemm_layout_ok(w))) {
         launch_gemm(g, w, in, out, tokens);
         return;

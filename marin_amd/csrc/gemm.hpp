@@ -29,6 +29,13 @@ bool gemm_layout_ok(const marin_quant_matrix *w);
 // the decode product; with out.argmax_each, the greedy choice of every token into out.argmax[t]); uses the
 // context's workspace for the activation limbs. Token blocks of 8 for up to 8 tokens, of 32 beyond.
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
+// Activation limbs of `tokens` rows (quantize_act): limbs [tokens][4][cols], the per-(token, group) factors
+// 2^-s [tokens][groups] and the RMSNorm factors [tokens] (1 without a norm), placed in the context's workspace.
+struct ActLimbs {
+    const int8_t *limbs;
+    const float *exps, *rs;
+};
+ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group);
 // Workspace bytes of launch_moe_gate_up (activation limbs of `tokens` rows of `cols`).
 size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group);
 // The grouped gate_up of a decode batch (2..MOE_BATCH tokens): every distinct selected expert's [2F][H] rows read
@@ -36,7 +43,10 @@ size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group);
 // [experts * 2F][H] matrix; `plan` as above, for at most `max_experts` distinct experts.
 void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *gate_up, const GemvIn &in, size_t tokens,
                         const int32_t *plan, size_t max_experts, size_t k, size_t ffn, float *act);
-// Any token count: the GEMM when it applies, else the decode product GEMV_TOKENS tokens at a time.
+// The product of a decode batch (gemv_batch.hip): 2..8 tokens, int8 codes, group 64 or 128.
+bool gemv_batch_supported(const marin_quant_matrix *w, size_t tokens);
+void launch_gemv_batch(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
+// Any token count: the batch product for 2..8 tokens, the GEMM when it applies, else the decode product GEMV_TOKENS tokens at a time.
 void launch_product(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
 
 }  // namespace marin

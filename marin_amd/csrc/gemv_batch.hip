@@ -1,0 +1,280 @@
+// The quantized product of a decode batch (2..8 tokens): the one-token product's schedule with the tokens' limbs
+// read from L2.
+//
+// Same exact arithmetic as the other products: codes are the A operand of v_mfma_i32_16x16x64_i8, the activations
+// are four signed 8-bit limbs per (token, group) (quantize_act), four tokens x four limbs fill the 16 B columns, so
+// a batch of up to 8 tokens takes two MFMAs per 64-column window of codes. Sums are exact int32 per group, scaled
+// once by weight scale x the token's 2^-s.
+//
+// Schedule (a batch must read the weights once and at the speed of the one-token product):
+//  - a persistent grid over 16-row tiles, 8 waves per block; wave w owns the fixed column slice [w S, (w + 1) S)
+//    windows of every row, so a tile's K is split over the waves and their sums meet in LDS once per tile;
+//  - a ring of RING items (tile, window) per wave runs across tile ends: the code window (HBM) and the B fragments
+//    of the window for each token tile (L2: every block reads the same few KiB of limbs) travel together;
+//  - every load is unconditional (clamped), so the waits are exact and never drain the ring;
+//  - epilogues: f32, residual add, SiLU(gate) * up, bf16, and the greedy choice of every token.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+
+#include "gemm.hpp"
+
+namespace marin {
+
+namespace {
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BW = 8;      // waves per block
+constexpr int BRING = 8;   // items in flight per wave
+constexpr int BATCH_BLOCKS_PER_CU = 2;
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ unsigned long long choice_key(float v, int row) {
+    const int b = __float_as_int(v);
+    const unsigned k = (unsigned)(b ^ (int)(((unsigned)(b >> 31)) >> 1)) ^ 0x80000000u;
+    return (unsigned long long)k << 32 | (unsigned long long)(0xffffffffu - (unsigned)row);
+}
+
+}  // namespace
+
+// WG: windows per quantization group; TT: token tiles of 4 (1 or 2); SM: windows per wave per tile; ST: scale type.
+template <int WG, int TT, int SM, typename ST>
+__global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
+                                                      const int8_t *__restrict__ limbs,
+                                                      const float *__restrict__ exps, const float *__restrict__ rsv,
+                                                      GemvOut out, int tokens, int rows, int cols, int tiles) {
+    constexpr int S = SM;
+    __shared__ __align__(16) float red[2][BW][4 * TT][16];
+    __shared__ unsigned long long best_s[4 * TT];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, q = lane >> 4;
+    const int windows = cols >> 6;
+    const int groups = windows / WG;
+    const size_t tile_bytes = (size_t)16 * cols;
+    const int w0 = wave * S;
+    const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int items = my_tiles * S;
+    if (threadIdx.x < 4 * TT) best_s[threadIdx.x] = 0ull;  // read after the tiles' barriers
+
+    // the epilogue's token factors, loaded before the ring: a load issued after it would wait for all of it
+    float rsl[TT];
+#pragma unroll
+    for (int pass = 0; pass < TT; ++pass) rsl[pass] = rsv[min(4 * pass + lane / 16, tokens - 1)];
+    // this lane's B column in token tile j: token 4 j + c / 4 (clamped to the batch), limb c % 4
+    const int8_t *brow[TT];
+    const float *erow[TT];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        const int tok = min(4 * j + c / 4, tokens - 1);
+        brow[j] = limbs + ((size_t)tok * 4 + (c & 3)) * cols + 16 * q;
+        erow[j] = exps + (size_t)tok * groups;
+    }
+
+    u32x4 ra[BRING];
+    u32x4 rb[BRING][TT];
+    floatx4 rs_[BRING / WG];
+    float re[BRING / WG][TT];
+    auto load_item = [&](int i, int slot) {
+        const int t = (int)blockIdx.x + (i / S) * (int)gridDim.x;
+        const int w = min(w0 + i % S, windows - 1);
+        ra[slot] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(codes + (size_t)t * tile_bytes + (size_t)w * 1024 + 16 * lane));
+#pragma unroll
+        for (int j = 0; j < TT; ++j) rb[slot][j] = *reinterpret_cast<const u32x4 *>(brow[j] + 64 * w);
+        if (slot % WG == 0) {
+            const ST *sp = scales + ((size_t)t * groups + w / WG) * 16 + 4 * q;
+            if constexpr (sizeof(ST) == 4) {
+                rs_[slot / WG] = *reinterpret_cast<const floatx4 *>(sp);
+            } else {
+                const uint2 sv = *reinterpret_cast<const uint2 *>(sp);
+                rs_[slot / WG] = (floatx4){__uint_as_float(sv.x << 16), __uint_as_float(sv.x & 0xffff0000u),
+                                           __uint_as_float(sv.y << 16), __uint_as_float(sv.y & 0xffff0000u)};
+            }
+#pragma unroll
+            for (int j = 0; j < TT; ++j) re[slot / WG][j] = erow[j][w / WG];
+        }
+    };
+    const int last = items > 0 ? items - 1 : 0;
+#pragma unroll
+    for (int j = 0; j < BRING; ++j) load_item(min(j, last), j);
+
+    floatx4 total[TT];
+    int4v acc[TT];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        total[j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        acc[j] = (int4v){0, 0, 0, 0};
+    }
+    floatx4 gsc = total[0];
+    float gex[TT];
+    int tile_n = 0;
+    const float lw = (c & 3) == 0 ? 1.0f : (c & 3) == 1 ? 256.0f : (c & 3) == 2 ? 65536.0f : 16777216.0f;
+    for (int base = 0; base < items; base += BRING) {
+#pragma unroll
+        for (int s = 0; s < BRING; ++s) {
+            const int i = base + s;
+            const int4v a = __builtin_bit_cast(int4v, ra[s]);
+            int4v b[TT];
+#pragma unroll
+            for (int j = 0; j < TT; ++j) b[j] = __builtin_bit_cast(int4v, rb[s][j]);
+            if (s % WG == 0) {
+                gsc = rs_[s / WG];
+#pragma unroll
+                for (int j = 0; j < TT; ++j) gex[j] = re[s / WG][j];
+            }
+            // items past the block's last one (the ring's tail) contribute zeros and end no tile
+            const bool valid = i < items;
+            const int wl = i % S;
+            const int w = w0 + wl;
+            const bool on = valid && w < windows;
+#pragma unroll
+            for (int j = 0; j < TT; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, on ? b[j] : (int4v){0, 0, 0, 0}, acc[j], 0, 0, 0);
+            // the slot is refilled once consumed, so its registers carry straight over to the next round
+            load_item(min(i + BRING, last), s);
+            if (s % WG == WG - 1) {
+                // end of a group: one conversion, scaled by weight scale x the token's 2^-s
+#pragma unroll
+                for (int j = 0; j < TT; ++j) {
+                    if (on) {
+                        const floatx4 f = (floatx4){(float)acc[j][0], (float)acc[j][1], (float)acc[j][2], (float)acc[j][3]};
+                        total[j] += f * (gsc * gex[j]);
+                    }
+                    acc[j] = (int4v){0, 0, 0, 0};
+                }
+            }
+            if (valid && wl == S - 1) {
+                // ---- end of a tile: limbs weighted 2^(8 l) and summed over a token's four lanes, then over the waves
+                float *rb_ = &red[tile_n & 1][0][0][0];
+#pragma unroll
+                for (int j = 0; j < TT; ++j) {
+                    float r4[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        float v = total[j][k] * lw;
+                        v += __shfl_xor(v, 1);
+                        v += __shfl_xor(v, 2);
+                        r4[k] = v;
+                    }
+                    if ((c & 3) == 0)
+                        *reinterpret_cast<float4 *>(rb_ + ((wave * 4 * TT) + 4 * j + c / 4) * 16 + 4 * q) =
+                            make_float4(r4[0], r4[1], r4[2], r4[3]);
+                    total[j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+                }
+                __syncthreads();
+                if (wave == 0) {
+                    // lane = (token tt, row r): 4 TT tokens x 16 rows over the wave's 64 lanes (and a second pass
+                    // for TT = 2)
+#pragma unroll
+                    for (int pass = 0; pass < TT; ++pass) {
+                        const int tt = 4 * pass + lane / 16, r = lane % 16;
+                        float v = 0.0f;
+#pragma unroll
+                        for (int ww = 0; ww < BW; ++ww) v += rb_[(ww * 4 * TT + tt) * 16 + r];
+                        const int t = (int)blockIdx.x + tile_n * (int)gridDim.x;
+                        const int row = t * 16 + r;
+                        const bool mine = tt < tokens;
+                        v *= rsl[pass];
+                        if (out.mode == OUT_SILU) {
+                            const float upv = __shfl_xor(v, 1);
+                            if (mine && (r & 1) == 0 && row < rows)
+                                reinterpret_cast<float *>(out.y)[(size_t)tt * out.y_stride + (row >> 1)] = silu_f(v) * upv;
+                        } else if (mine && row < rows) {
+                            const size_t at = (size_t)tt * out.y_stride + row;
+                            if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v;
+                            else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v;
+                            else {
+                                const unsigned uu = __float_as_uint(v);
+                                reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
+                                    (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
+                                                                     : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+                            }
+                        }
+                        if (out.argmax_each) {
+                            // the token's 16 rows (lanes 16 (tt % 4) ..) reduced by shuffles, one LDS max per token
+                            unsigned long long key = mine && row < rows ? choice_key(v, row) : 0ull;
+#pragma unroll
+                            for (int o = 1; o < 16; o <<= 1) {
+                                const unsigned long long other = __shfl_xor(key, o);
+                                key = other > key ? other : key;
+                            }
+                            if (r == 0 && key) atomicMax(&best_s[tt], key);
+                        }
+                    }
+                }
+                ++tile_n;
+            }
+        }
+    }
+    if (out.argmax_each) {
+        __syncthreads();
+        if ((int)threadIdx.x < 4 * TT && (int)threadIdx.x < tokens && best_s[threadIdx.x])
+            atomicMax(out.argmax + threadIdx.x, best_s[threadIdx.x]);
+    }
+}
+
+// Windows per wave per tile: the smallest instantiated width whose BW slices cover the row, 0 when none does.
+static int batch_slice(int windows) {
+    for (int sm : {4, 8, 12, 24})
+        if (BW * sm >= windows) return sm;
+    return 0;
+}
+
+bool gemv_batch_supported(const marin_quant_matrix *w, size_t tokens) {
+    return tokens >= 2 && tokens <= 8 && gemm_layout_ok(w) && batch_slice((int)(w->cols / 64)) > 0;
+}
+
+template <int WG, int TT, int SM, typename ST>
+static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
+    const int tiles = (int)(w->rows_padded / 16);
+    auto kern = gemv_batch<WG, TT, SM, ST>;
+    int resident = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * BW, 0) != hipSuccess || resident < 1)
+        resident = 1;
+    const int blocks = std::min(tiles, std::min(resident, BATCH_BLOCKS_PER_CU) * std::max(g->cu_count, 1));
+    kern<<<dim3((unsigned)blocks), dim3(64 * BW), 0, g->stream>>>(w->codes, (const ST *)w->scales, al.limbs, al.exps,
+                                                                   al.rs, out, (int)tokens, (int)w->rows,
+                                                                   (int)w->cols, tiles);
+}
+
+template <int WG, int TT, typename ST>
+static void launch_sm(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
+    switch (batch_slice((int)(w->cols / 64))) {
+        case 4: launch_t<WG, TT, 4, ST>(g, w, al, out, tokens); break;
+        case 8: launch_t<WG, TT, 8, ST>(g, w, al, out, tokens); break;
+        case 12: launch_t<WG, TT, 12, ST>(g, w, al, out, tokens); break;
+        default: launch_t<WG, TT, 24, ST>(g, w, al, out, tokens); break;
+    }
+}
+
+template <typename ST>
+static void launch_st(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
+    const bool wg2 = w->group == 128;
+    if (tokens <= 4) {
+        if (wg2) launch_sm<2, 1, ST>(g, w, al, out, tokens);
+        else launch_sm<1, 1, ST>(g, w, al, out, tokens);
+    } else {
+        if (wg2) launch_sm<2, 2, ST>(g, w, al, out, tokens);
+        else launch_sm<1, 2, ST>(g, w, al, out, tokens);
+    }
+}
+
+void launch_gemv_batch(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
+    if (!gemv_batch_supported(w, tokens)) unsupported("batch product (2..8 tokens, int8, group 64 or 128)", 8, tokens);
+    if (out.argmax && !out.argmax_each) unsupported("batch product greedy choice (one per token only)", 1, 0);
+    const ActLimbs al = launch_quantize_act(g, in, tokens, w->cols, w->group);
+    if (w->bf16_scales) launch_st<uint16_t>(g, w, al, out, tokens);
+    else launch_st<float>(g, w, al, out, tokens);
+    const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;
+    const double outs = out.mode == OUT_SILU ? (double)w->rows / 2 : (double)w->rows;
+    const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * w->groups() * (w->bf16_scales ? 2 : 4) +
+                         (double)tokens * w->cols * act + (double)tokens * outs * res;
+    g->launched(marin_gpu::GEMV, bytes, "gemv_batch");
+}
+
+}  // namespace marin
