@@ -42,9 +42,13 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 }  // namespace
 
 // One token row per workgroup. GCOLS = quantization group width (a multiple of 4, at most 4 * 64).
-template <int GCOLS>
+// FRAG false: limbs [token][limb][column]. FRAG true (the batch product): the limbs already in B-operand order,
+// [window][token tile][64 lanes][16 bytes] with lane 16 q + 4 (token % 4) + limb holding columns 64 w + 16 q .. + 16,
+// so each B fragment is one contiguous KiB; `ttiles` = token tiles of 4.
+template <int GCOLS, bool FRAG>
 __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, int8_t *__restrict__ limbs,
-                                                           float *__restrict__ exps, float *__restrict__ rs_out) {
+                                                           float *__restrict__ exps, float *__restrict__ rs_out,
+                                                           int ttiles) {
     constexpr int TPG = GCOLS / 4;  // threads per group, 4 consecutive columns each
     static_assert(TPG <= 64 && (TPG & (TPG - 1)) == 0, "group width");
     __shared__ float red[QA_THREADS / 64];
@@ -122,8 +126,16 @@ __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, 
             }
         }
 #pragma unroll
-        for (int l = 0; l < 4; ++l)
-            *reinterpret_cast<uint32_t *>(limbs + ((size_t)t * 4 + l) * cols + k) = word[l];
+        for (int l = 0; l < 4; ++l) {
+            size_t at;
+            if constexpr (FRAG) {
+                const int lane = ((k & 63) >> 4) * 16 + (t & 3) * 4 + l;
+                at = (((size_t)(k >> 6) * ttiles + (t >> 2)) * 64 + lane) * 16 + (k & 15);
+            } else {
+                at = ((size_t)t * 4 + l) * cols + k;
+            }
+            *reinterpret_cast<uint32_t *>(limbs + at) = word[l];
+        }
         if ((threadIdx.x % TPG) == 0) exps[(size_t)t * groups + g] = ldexpf(1.0f, -sh);
     }
 }
@@ -400,8 +412,8 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     int8_t *limbs = (int8_t *)ws;
     float *exps = (float *)(ws + limb_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
-    if (w->group == 128) quantize_act<128><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
-    else quantize_act<64><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    if (w->group == 128) quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+    else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
     g->launched();
     const bool wg2 = w->group == 128;
     if (w->bf16_scales) {
@@ -424,14 +436,23 @@ size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group) {
     return align16(tokens * 4 * cols) + align16(tokens * (cols / group) * 4) + tokens * 4;
 }
 
-ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group) {
-    const size_t limb_bytes = align16(tokens * 4 * cols), exp_bytes = align16(tokens * (cols / group) * 4);
-    uint8_t *ws = (uint8_t *)g->workspace(moe_gate_up_workspace(tokens, cols, group));
+ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group, bool frag) {
+    // fragment order pads the tokens to whole tiles of 4 (the padding is never read: lanes of missing tokens read a
+    // real token's fragment)
+    const size_t ttiles = (tokens + 3) / 4;
+    const size_t limb_bytes = align16((frag ? ttiles * 4 : tokens) * 4 * cols), exp_bytes = align16(tokens * (cols / group) * 4);
+    uint8_t *ws = (uint8_t *)g->workspace(moe_gate_up_workspace(frag ? ttiles * 4 : tokens, cols, group));
     int8_t *limbs = (int8_t *)ws;
     float *exps = (float *)(ws + limb_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
-    if (group == 128) quantize_act<128><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
-    else quantize_act<64><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    const unsigned tt = (unsigned)ttiles;
+    if (group == 128) {
+        if (frag) quantize_act<128, true><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+        else quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+    } else {
+        if (frag) quantize_act<64, true><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+        else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+    }
     g->launched();
     return ActLimbs{limbs, exps, rs};
 }
@@ -461,8 +482,8 @@ void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *w, const GemvIn 
     int8_t *limbs = (int8_t *)ws;
     float *exps = (float *)(ws + limb_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
-    if (w->group == 128) quantize_act<128><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
-    else quantize_act<64><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs);
+    if (w->group == 128) quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+    else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
     g->launched();
     MoePlanView pv;
     pv.plan = plan;

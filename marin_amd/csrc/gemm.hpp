@@ -29,13 +29,14 @@ bool gemm_layout_ok(const marin_quant_matrix *w);
 // the decode product; with out.argmax_each, the greedy choice of every token into out.argmax[t]); uses the
 // context's workspace for the activation limbs. Token blocks of 8 for up to 8 tokens, of 32 beyond.
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens);
-// Activation limbs of `tokens` rows (quantize_act): limbs [tokens][4][cols], the per-(token, group) factors
+// Activation limbs of `tokens` rows (quantize_act): limbs [tokens][4][cols] (or fragment order, below), the per-(token, group) factors
 // 2^-s [tokens][groups] and the RMSNorm factors [tokens] (1 without a norm), placed in the context's workspace.
 struct ActLimbs {
     const int8_t *limbs;
     const float *exps, *rs;
 };
-ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group);
+// With `frag`, the limbs in B-operand fragment order instead ([window][token tile][64 lanes][16 bytes]).
+ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group, bool frag);
 // Workspace bytes of launch_moe_gate_up (activation limbs of `tokens` rows of `cols`).
 size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group);
 // The grouped gate_up of a decode batch (2..MOE_BATCH tokens): every distinct selected expert's [2F][H] rows read

@@ -12,7 +12,8 @@
 //  - a ring of RING items (tile, window) per wave runs across tile ends: the code window (HBM) and the B fragments
 //    of the window for each token tile (L2: every block reads the same few KiB of limbs) travel together;
 //  - every load is unconditional (clamped), so the waits are exact and never drain the ring;
-//  - epilogues: f32, residual add, SiLU(gate) * up, bf16, and the greedy choice of every token.
+//  - the loop touches global memory only through the ring: a tile's finished rows go to an LDS buffer and are
+//    written out (f32, residual add, SiLU(gate) * up, bf16, the greedy choice of every token) after the loop.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -29,8 +30,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BW = 8;      // waves per block
-constexpr int BRING = 8;   // items in flight per wave
+// items in flight per wave: 8 for one token tile; 6 for two, so two blocks stay resident per compute unit
+template <int TT>
+constexpr int bring() { return TT == 1 ? 8 : 6; }
 constexpr int BATCH_BLOCKS_PER_CU = 2;
+constexpr int OBUF_TILES = 40;  // tiles a block holds outputs for (the grid covers the matrix in as many rounds)
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
@@ -44,12 +48,16 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 
 // WG: windows per quantization group; TT: token tiles of 4 (1 or 2); SM: windows per wave per tile; ST: scale type.
 template <int WG, int TT, int SM, typename ST>
-__global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
+__global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                       const int8_t *__restrict__ limbs,
                                                       const float *__restrict__ exps, const float *__restrict__ rsv,
                                                       GemvOut out, int tokens, int rows, int cols, int tiles) {
     constexpr int S = SM;
+    constexpr int BRING = bring<TT>();
     __shared__ __align__(16) float red[2][BW][4 * TT][16];
+    // the block's finished rows, written out after the main loop: a global store or load inside the loop would
+    // sit in the vector memory counter with the ring and make the waits for it drain the ring
+    __shared__ float obuf[OBUF_TILES][4 * TT][16];
     __shared__ unsigned long long best_s[4 * TT];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -66,13 +74,16 @@ __global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict_
     float rsl[TT];
 #pragma unroll
     for (int pass = 0; pass < TT; ++pass) rsl[pass] = rsv[min(4 * pass + lane / 16, tokens - 1)];
-    // this lane's B column in token tile j: token 4 j + c / 4 (clamped to the batch), limb c % 4
+    // the limbs are in B-fragment order ([window][token tile][lane][16 bytes]); this lane's token in token tile j is
+    // 4 j + c / 4, and a lane of a token past the batch reads the batch's last token (its sums are never written)
+    const int ttiles = (tokens + 3) / 4;
     const int8_t *brow[TT];
     const float *erow[TT];
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
         const int tok = min(4 * j + c / 4, tokens - 1);
-        brow[j] = limbs + ((size_t)tok * 4 + (c & 3)) * cols + 16 * q;
+        const int ln = tok == 4 * j + c / 4 ? lane : 16 * q + 4 * (tok & 3) + (c & 3);
+        brow[j] = limbs + ((size_t)(tok >> 2) * 64 + ln) * 16;
         erow[j] = exps + (size_t)tok * groups;
     }
 
@@ -86,8 +97,8 @@ __global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict_
         ra[slot] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4 *>(codes + (size_t)t * tile_bytes + (size_t)w * 1024 + 16 * lane));
 #pragma unroll
-        for (int j = 0; j < TT; ++j) rb[slot][j] = *reinterpret_cast<const u32x4 *>(brow[j] + 64 * w);
-        if (slot % WG == 0) {
+        for (int j = 0; j < TT; ++j) rb[slot][j] = *reinterpret_cast<const u32x4 *>(brow[j] + (size_t)w * ttiles * 1024);
+        if (slot % WG == WG - 1) {  // the group's factors travel with its last window, read at the group's end
             const ST *sp = scales + ((size_t)t * groups + w / WG) * 16 + 4 * q;
             if constexpr (sizeof(ST) == 4) {
                 rs_[slot / WG] = *reinterpret_cast<const floatx4 *>(sp);
@@ -111,8 +122,6 @@ __global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict_
         total[j] = (floatx4){0.f, 0.f, 0.f, 0.f};
         acc[j] = (int4v){0, 0, 0, 0};
     }
-    floatx4 gsc = total[0];
-    float gex[TT];
     int tile_n = 0;
     const float lw = (c & 3) == 0 ? 1.0f : (c & 3) == 1 ? 256.0f : (c & 3) == 2 ? 65536.0f : 16777216.0f;
     for (int base = 0; base < items; base += BRING) {
@@ -123,11 +132,6 @@ __global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict_
             int4v b[TT];
 #pragma unroll
             for (int j = 0; j < TT; ++j) b[j] = __builtin_bit_cast(int4v, rb[s][j]);
-            if (s % WG == 0) {
-                gsc = rs_[s / WG];
-#pragma unroll
-                for (int j = 0; j < TT; ++j) gex[j] = re[s / WG][j];
-            }
             // items past the block's last one (the ring's tail) contribute zeros and end no tile
             const bool valid = i < items;
             const int wl = i % S;
@@ -135,15 +139,15 @@ __global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict_
             const bool on = valid && w < windows;
 #pragma unroll
             for (int j = 0; j < TT; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, on ? b[j] : (int4v){0, 0, 0, 0}, acc[j], 0, 0, 0);
-            // the slot is refilled once consumed, so its registers carry straight over to the next round
-            load_item(min(i + BRING, last), s);
             if (s % WG == WG - 1) {
                 // end of a group: one conversion, scaled by weight scale x the token's 2^-s
+                const floatx4 gsc = rs_[s / WG];
 #pragma unroll
                 for (int j = 0; j < TT; ++j) {
+                    const float gex = re[s / WG][j];
                     if (on) {
                         const floatx4 f = (floatx4){(float)acc[j][0], (float)acc[j][1], (float)acc[j][2], (float)acc[j][3]};
-                        total[j] += f * (gsc * gex[j]);
+                        total[j] += f * (gsc * gex);
                     }
                     acc[j] = (int4v){0, 0, 0, 0};
                 }
@@ -168,47 +172,56 @@ __global__ __launch_bounds__(64 * BW) void gemv_batch(const uint8_t *__restrict_
                 }
                 __syncthreads();
                 if (wave == 0) {
-                    // lane = (token tt, row r): 4 TT tokens x 16 rows over the wave's 64 lanes (and a second pass
-                    // for TT = 2)
+                    // lane = (token tt, row r): 4 TT tokens x 16 rows over the wave's 64 lanes (a second pass for
+                    // TT = 2); the tile's sums times the token's norm factor into the output buffer
 #pragma unroll
                     for (int pass = 0; pass < TT; ++pass) {
                         const int tt = 4 * pass + lane / 16, r = lane % 16;
                         float v = 0.0f;
 #pragma unroll
                         for (int ww = 0; ww < BW; ++ww) v += rb_[(ww * 4 * TT + tt) * 16 + r];
-                        const int t = (int)blockIdx.x + tile_n * (int)gridDim.x;
-                        const int row = t * 16 + r;
-                        const bool mine = tt < tokens;
-                        v *= rsl[pass];
-                        if (out.mode == OUT_SILU) {
-                            const float upv = __shfl_xor(v, 1);
-                            if (mine && (r & 1) == 0 && row < rows)
-                                reinterpret_cast<float *>(out.y)[(size_t)tt * out.y_stride + (row >> 1)] = silu_f(v) * upv;
-                        } else if (mine && row < rows) {
-                            const size_t at = (size_t)tt * out.y_stride + row;
-                            if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v;
-                            else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v;
-                            else {
-                                const unsigned uu = __float_as_uint(v);
-                                reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
-                                    (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
-                                                                     : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
-                            }
-                        }
-                        if (out.argmax_each) {
-                            // the token's 16 rows (lanes 16 (tt % 4) ..) reduced by shuffles, one LDS max per token
-                            unsigned long long key = mine && row < rows ? choice_key(v, row) : 0ull;
-#pragma unroll
-                            for (int o = 1; o < 16; o <<= 1) {
-                                const unsigned long long other = __shfl_xor(key, o);
-                                key = other > key ? other : key;
-                            }
-                            if (r == 0 && key) atomicMax(&best_s[tt], key);
-                        }
+                        obuf[tile_n][tt][r] = v * rsl[pass];
                     }
                 }
                 ++tile_n;
             }
+            // the slot is refilled once everything in it is consumed, so its registers carry straight over to the
+            // next round
+            load_item(min(i + BRING, last), s);
+        }
+    }
+    __syncthreads();
+    // ---- outputs: thread per (tile, token, row pair)
+    const int pairs = my_tiles * 4 * TT * 8;
+    for (int p = (int)threadIdx.x; p < pairs; p += 64 * BW) {
+        const int tn = p / (4 * TT * 8), tt = (p / 8) % (4 * TT), r = 2 * (p % 8);
+        const int row = ((int)blockIdx.x + tn * (int)gridDim.x) * 16 + r;
+        if (tt >= tokens) continue;
+        const float v0 = obuf[tn][tt][r], v1 = obuf[tn][tt][r + 1];
+        if (out.mode == OUT_SILU) {
+            if (row < rows) reinterpret_cast<float *>(out.y)[(size_t)tt * out.y_stride + (row >> 1)] = silu_f(v0) * v1;
+            continue;
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float v = k ? v1 : v0;
+            if (row + k >= rows) continue;
+            const size_t at = (size_t)tt * out.y_stride + row + k;
+            if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v;
+            else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v;
+            else {
+                const unsigned uu = __float_as_uint(v);
+                reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
+                    (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+            }
+        }
+        if (out.argmax_each) {
+            unsigned long long key = row < rows ? choice_key(v0, row) : 0ull;
+            if (row + 1 < rows) {
+                const unsigned long long k1 = choice_key(v1, row + 1);
+                key = k1 > key ? k1 : key;
+            }
+            if (key) atomicMax(&best_s[tt], key);
         }
     }
     if (out.argmax_each) {
@@ -236,7 +249,8 @@ static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &
     int resident = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * BW, 0) != hipSuccess || resident < 1)
         resident = 1;
-    const int blocks = std::min(tiles, std::min(resident, BATCH_BLOCKS_PER_CU) * std::max(g->cu_count, 1));
+    const int blocks = std::max(std::min(tiles, std::min(resident, BATCH_BLOCKS_PER_CU) * std::max(g->cu_count, 1)),
+                                (tiles + OBUF_TILES - 1) / OBUF_TILES);
     kern<<<dim3((unsigned)blocks), dim3(64 * BW), 0, g->stream>>>(w->codes, (const ST *)w->scales, al.limbs, al.exps,
                                                                    al.rs, out, (int)tokens, (int)w->rows,
                                                                    (int)w->cols, tiles);
@@ -267,7 +281,7 @@ static void launch_st(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs 
 void launch_gemv_batch(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     if (!gemv_batch_supported(w, tokens)) unsupported("batch product (2..8 tokens, int8, group 64 or 128)", 8, tokens);
     if (out.argmax && !out.argmax_each) unsupported("batch product greedy choice (one per token only)", 1, 0);
-    const ActLimbs al = launch_quantize_act(g, in, tokens, w->cols, w->group);
+    const ActLimbs al = launch_quantize_act(g, in, tokens, w->cols, w->group, true);
     if (w->bf16_scales) launch_st<uint16_t>(g, w, al, out, tokens);
     else launch_st<float>(g, w, al, out, tokens);
     const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;

@@ -848,7 +848,7 @@ marin_status marin_qwen3_batch_decode(marin_qwen3_batch *b, size_t steps, uint32
         }
         // the products' activation limbs: grown before a capture (a capture may not allocate)
         const auto &cfg = m->cfg;
-        g->workspace(moe_gate_up_workspace(B, std::max(std::max(cfg.hidden, cfg.ffn), m->qd()), cfg.group));
+        g->workspace(moe_gate_up_workspace((B + 3) / 4 * 4, std::max(std::max(cfg.hidden, cfg.ffn), m->qd()), cfg.group));
         if (graphs_enabled()) {
             if (!b->graph) {
                 hipGraph_t graph;
