@@ -140,6 +140,97 @@ __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, 
     }
 }
 
+// The same limbs in one pass, for short rows of a decode batch (the batch product's B fragments): one token per
+// workgroup of 1024 threads, thread T holding columns 4 T + 4096 i (i < IT) in registers from a single load burst
+// (the row and its norm weights), one block reduction for the RMSNorm statistic, then the limbs in fragment order.
+constexpr int QR_THREADS = 1024;
+template <int GCOLS, int IT>
+__global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols, int8_t *__restrict__ limbs,
+                                                            float *__restrict__ exps, float *__restrict__ rs_out,
+                                                            int ttiles) {
+    constexpr int TPG = GCOLS / 4;
+    __shared__ float red[QR_THREADS / 64];
+    const int t = blockIdx.x;
+    const int groups = cols / GCOLS;
+    const bool norm = in.mode == IN_NORM;
+    float v[IT][4], w[IT][4];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int k = min(4 * ((int)threadIdx.x + QR_THREADS * it), cols - 4);  // clamped: loads stay unconditional
+        if (in.mode == IN_BF16) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(in.x) + (size_t)t * in.x_stride + k);
+            v[it][0] = __uint_as_float(u.x << 16);
+            v[it][1] = __uint_as_float(u.x & 0xffff0000u);
+            v[it][2] = __uint_as_float(u.y << 16);
+            v[it][3] = __uint_as_float(u.y & 0xffff0000u);
+        } else {
+            const float4 f = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(in.x) + (size_t)t * in.x_stride + k);
+            v[it][0] = f.x;
+            v[it][1] = f.y;
+            v[it][2] = f.z;
+            v[it][3] = f.w;
+        }
+        const float4 nw = *reinterpret_cast<const float4 *>(norm ? in.norm + k : reinterpret_cast<const float *>(in.x) + k);
+        w[it][0] = nw.x;
+        w[it][1] = nw.y;
+        w[it][2] = nw.z;
+        w[it][3] = nw.w;
+    }
+    float rs = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < IT; ++it)
+            if (4 * ((int)threadIdx.x + QR_THREADS * it) < cols)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ss += v[it][e] * v[it][e];
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < QR_THREADS / 64; ++i) total += red[i];
+        rs = 1.0f / sqrtf(total / (float)cols + in.eps);
+    }
+    if (threadIdx.x == 0) rs_out[t] = rs;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int k = 4 * ((int)threadIdx.x + QR_THREADS * it);
+        const bool on = k < cols;
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = on ? (norm ? v[it][e] * w[it][e] : v[it][e]) : 0.0f;
+        float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        for (int o = 1; o < TPG; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        int sh = 0;
+        if (mx > 0.0f && mx < INFINITY) {
+            int e;
+            (void)frexpf(mx, &e);
+            sh = 30 - e;
+            sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+        }
+        if (!on) continue;
+        const float up = ldexpf(1.0f, sh);
+        uint32_t word[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int xi = __float2int_rn(x[e] * up);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int lb = l == 3 ? xi : (int)(int8_t)(xi & 0xff);
+                word[l] |= ((uint32_t)lb & 0xffu) << (8 * e);
+                xi = (xi - lb) >> 8;
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int lane = ((k & 63) >> 4) * 16 + (t & 3) * 4 + l;
+            *reinterpret_cast<uint32_t *>(limbs + (((size_t)(k >> 6) * ttiles + (t >> 2)) * 64 + lane) * 16 + (k & 15)) = word[l];
+        }
+        if ((threadIdx.x % TPG) == 0) exps[(size_t)t * groups + k / GCOLS] = ldexpf(1.0f, -sh);
+    }
+}
+
 // WG: 64-column windows per group; TOK: tokens per workgroup (a multiple of 4).
 // Prompt GEMM (MOE false): grid (row blocks of 128, token blocks of TOK).
 // Grouped expert product (MOE true, gate_up of a decode batch of at most TOK tokens): grid (row blocks of 128 of
@@ -446,6 +537,27 @@ ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size
     float *exps = (float *)(ws + limb_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
     const unsigned tt = (unsigned)ttiles;
+    if (frag && cols <= 4 * 4096) {
+        const unsigned nt = (unsigned)tokens;
+        const int it = (int)((cols + 4095) / 4096);
+        if (group == 128) {
+            switch (it) {
+                case 1: quantize_rows<128, 1><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                case 2: quantize_rows<128, 2><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                case 3: quantize_rows<128, 3><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                default: quantize_rows<128, 4><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+            }
+        } else {
+            switch (it) {
+                case 1: quantize_rows<64, 1><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                case 2: quantize_rows<64, 2><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                case 3: quantize_rows<64, 3><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                default: quantize_rows<64, 4><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+            }
+        }
+        g->launched();
+        return ActLimbs{limbs, exps, rs};
+    }
     if (group == 128) {
         if (frag) quantize_act<128, true><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
         else quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
