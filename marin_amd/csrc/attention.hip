@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "attention.hpp"
@@ -203,7 +204,10 @@ extern "C" void marin_attn_dbg_clear() {
 // FUSE: q and the new tokens' keys and values are the raw projections [tokens][heads + 2 kv_heads][hd]; the kernel
 // applies q/k RMSNorm and RoPE itself and stores the new keys and values of its chunk into the cache before reading
 // it (every row group of the chunk stores the same bytes).
-constexpr int POS_IN_FLIGHT = 2;  // positions per lane group loaded together
+#ifndef ATTN_POS_IN_FLIGHT
+#define ATTN_POS_IN_FLIGHT 2
+#endif
+constexpr int POS_IN_FLIGHT = ATTN_POS_IN_FLIGHT;  // positions per lane group loaded together
 constexpr int GROUP = 16;         // chunks merged together at the first level
 
 // Records: [max, sum, 0, 0, values, pad] of rec_floats(hd) floats (a multiple of 4), written and read with 16-byte
@@ -1208,6 +1212,11 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     }
     // the fused inputs of attention_split are one sequence's token rows
     if (a.fuse.qkv && a.batch > 1) unsupported("fused attention over a batch (one-token decode only)", 1, a.batch);
+    if (prefill_fa_fits(a) && !getenv("MARIN_NO_FA")) {
+        if (g->only && strcmp(g->only, "fa_prefill")) return;
+        launch_prefill_fa(g, a);
+        return;
+    }
     if (g->only && strcmp(g->only, "attention_split")) return;
     dim3 grid((unsigned)splits, (unsigned)(a.kv_heads * row_groups), (unsigned)a.batch);
     switch (a.geom.format) {

@@ -89,6 +89,12 @@ size_t attention_partial_floats(size_t batch, size_t tokens, size_t heads, size_
                                 int cu_count);
 // Chunk counters a launch of `batch` sequences of `tokens` new tokens can use.
 size_t attention_counters(size_t batch, size_t tokens, size_t heads);
+
+// Prompt attention on the matrix cores (attention_fa.hip): one sequence, 16+ tokens, f16 cache, head size 64 or 128,
+// 1, 2, 4 or 8 q heads per kv head; its q scratch lives in the partial records.
+size_t prefill_fa_scratch(size_t tokens, size_t heads, size_t hd);
+bool prefill_fa_fits(const AttentionArgs &a);
+void launch_prefill_fa(marin_gpu *g, const AttentionArgs &a);
 void launch_attention(marin_gpu *g, const AttentionArgs &a);
 
 // Stores f32 keys/values [tokens][kv_heads*head_dim] at positions start.. of one layer.

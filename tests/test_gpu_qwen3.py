@@ -87,16 +87,19 @@ def test_synthetic_greedy_tokens_match_the_golden(gpu, name, monkeypatch):
         logits = model.forward([g["tokens"][s]], cache)
 
 
-def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu):
+@pytest.mark.parametrize("fmt", [m.KvFormat.F32, m.KvFormat.F16])
+def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu, fmt):
     """A 300-token prompt runs as passes of at most the library's prompt chunk (128 tokens: 128, 128, 44), each
-    seeing the keys of the ones before; the greedy continuation and its top logits match the oracle's prompt pass."""
+    seeing the keys of the ones before; the greedy continuation and its top logits match the oracle's prompt pass.
+    With f16 keys and values the chunks' attention runs on the matrix cores."""
     g = golden("mini")
     shape = g["shape"]
     prompt = o.synth_prompt(g["seed"] + 7, 300, shape["vocab"]).tolist()
     steps = 6
-    toks, gaps, top_ids, top_vals = o.synth_greedy(shape, g["seed"], prompt, steps, with_top=True)
+    toks, gaps, top_ids, top_vals = o.synth_greedy(shape, g["seed"], prompt, steps, kv_f16=fmt == m.KvFormat.F16,
+                                                   with_top=True)
     model = Qwen3(gpu, shape, seed=g["seed"])
-    cache = model.new_cache(len(prompt) + steps + 1)
+    cache = model.new_cache(len(prompt) + steps + 1, fmt)
     logits = model.forward(prompt, cache)
     for s in range(steps):
         vals = np.asarray(top_vals[s], np.float64)
@@ -104,6 +107,25 @@ def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu):
         if gaps[s] > 1e-3:
             assert o.argmax(logits) == toks[s], s
         logits = model.forward([int(toks[s])], cache)
+
+
+@pytest.mark.parametrize("name", ["mini_f16kv", "1.7b"])
+def test_prompt_attention_on_the_matrix_cores_equals_the_vector_path(gpu, name, monkeypatch):
+    """The f16-cache prompt pass with its attention on the matrix cores (q and P split into two f16 parts each)
+    against the same pass on the vector-ALU attention: the logits agree to f32 accuracy."""
+    g = golden(name)
+    shape = g["shape"]
+    prompt = o.synth_prompt(g["seed"] + 3, 150, shape["vocab"]).tolist()
+    model = Qwen3(gpu, shape, seed=g["seed"])
+    out = []
+    for fa in ("0", "1"):
+        if fa == "1":
+            monkeypatch.setenv("MARIN_NO_FA", "1")
+        else:
+            monkeypatch.delenv("MARIN_NO_FA", raising=False)
+        out.append(model.forward(prompt, model.new_cache(len(prompt) + 1, m.KvFormat.F16)))
+    monkeypatch.delenv("MARIN_NO_FA", raising=False)
+    assert np.abs(out[0] - out[1]).max() <= 2e-4 * (1 + np.abs(out[1]).max())
 
 
 def agree_until_a_near_tie(got, exp, gaps, tie=1e-3):
