@@ -30,7 +30,7 @@ using namespace marin;
 namespace marin {
 
 #ifndef MARIN_PREFILL_CHUNK
-#define MARIN_PREFILL_CHUNK 128
+#define MARIN_PREFILL_CHUNK 512
 #endif
 constexpr size_t CHUNK = MARIN_PREFILL_CHUNK;  // tokens per prompt pass through the layers (the products run as GEMMs)
 

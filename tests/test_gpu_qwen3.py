@@ -89,12 +89,12 @@ def test_synthetic_greedy_tokens_match_the_golden(gpu, name, monkeypatch):
 
 @pytest.mark.parametrize("fmt", [m.KvFormat.F32, m.KvFormat.F16])
 def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu, fmt):
-    """A 300-token prompt runs as passes of at most the library's prompt chunk (128 tokens: 128, 128, 44), each
+    """A 600-token prompt runs as passes of at most the library's prompt chunk (512 tokens: 512, 88), each
     seeing the keys of the ones before; the greedy continuation and its top logits match the oracle's prompt pass.
     With f16 keys and values the chunks' attention runs on the matrix cores."""
     g = golden("mini")
     shape = g["shape"]
-    prompt = o.synth_prompt(g["seed"] + 7, 300, shape["vocab"]).tolist()
+    prompt = o.synth_prompt(g["seed"] + 7, 600, shape["vocab"]).tolist()
     steps = 6
     toks, gaps, top_ids, top_vals = o.synth_greedy(shape, g["seed"], prompt, steps, kv_f16=fmt == m.KvFormat.F16,
                                                    with_top=True)
