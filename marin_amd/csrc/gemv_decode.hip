@@ -168,7 +168,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     for (int j = 0; j < RING; ++j) load_item(min(j, last), j);
     TRACE(2);
 
-    // ---- prologue: RMSNorm statistic (the threads' columns cover the row once), then the limbs
+    // ---- prologue: the limbs (and the RMSNorm partial sums: the threads' columns cover the row once)
     float xv[R][16];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -185,7 +185,8 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     auto in_row = [&](int r) {  // this thread's columns lie in the row
         return r * 8192 + 16 * (int)threadIdx.x < cols;
     };
-    float rs = 1.0f;
+    // the RMSNorm statistic: the waves' partial sums meet at the prologue's barrier; the limbs hold x * weight, and
+    // the factor 1 / sqrt(mean(x^2) + eps) multiplies each row's sum at the end, so no barrier waits for it here
     if (norm) {
         float ss = 0.0f;
 #pragma unroll
@@ -195,11 +196,6 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
                 for (int e = 0; e < 16; ++e) ss += xv[r][e] * xv[r][e];
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
         if (lane == 0) ssq[wave] = ss;
-        __syncthreads();
-        float total = 0.0f;
-#pragma unroll
-        for (int w = 0; w < DW; ++w) total += ssq[w];
-        rs = 1.0f / sqrtf(total / (float)cols + in.eps);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -211,7 +207,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             float x = xv[r][e];
-            if (norm) x = x * rs * __uint_as_float(nr[r][e / 4][e % 4]);
+            if (norm) x = x * __uint_as_float(nr[r][e / 4][e % 4]);
             v[e] = x;
             mx = fmaxf(mx, fabsf(x));
         }
@@ -264,6 +260,13 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     TRACE(4);
     __syncthreads();
     TRACE(5);
+    float rs = 1.0f;
+    if (norm) {
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < DW; ++w) total += ssq[w];
+        rs = 1.0f / sqrtf(total / (float)cols + in.eps);
+    }
 
     floatx4 total = (floatx4){0.f, 0.f, 0.f, 0.f};
     floatx4 gsc = total;
@@ -324,6 +327,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
                     float v = 0.0f;
 #pragma unroll
                     for (int ww = 0; ww < DW; ++ww) v += rb[ww * 16 + lane];
+                    v *= rs;
                     const int t = (int)blockIdx.x + tile_n * (int)gridDim.x;
                     const int row = t * 16 + lane;
                     if (out.mode == OUT_SILU) {
