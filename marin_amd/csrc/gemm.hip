@@ -26,8 +26,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int QA_THREADS = 256;
-constexpr int GM_WAVES = 4;
+constexpr int GM_WAVES = 4;       // waves along the rows (128 rows per workgroup)
 constexpr int GM_ROW_TILES = 2;   // 16-row tiles per wave
+// Token halves of a workgroup: blocks of 64+ tokens take two sets of row waves, one per 32 tokens, so each code
+// window a workgroup reads from memory serves 64 tokens (the second wave's load of it hits the caches).
+__host__ __device__ constexpr int gm_halves(int tok) { return tok >= 64 ? tok / 32 : 1; }
 constexpr int GM_TOKENS = 32;     // tokens per workgroup of the prompt GEMM
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
@@ -238,13 +241,15 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols,
 // token and writes SiLU(gate) * up of the tokens that selected it into their (token, slot) activation rows. `tiles`
 // is then the tiles of one expert.
 template <int WG, typename ST, int TOK, bool MOE>
-__global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restrict__ codes,
+__global__ __launch_bounds__(64 * GM_WAVES * gm_halves(TOK)) void gemm_q8(const uint8_t *__restrict__ codes,
                                                          const ST *__restrict__ scales,
                                                          const int8_t *__restrict__ limbs,
                                                          const float *__restrict__ exps,
                                                          const float *__restrict__ rsv, GemvOut out, int tokens,
                                                          int rows, int cols, int tiles, MoePlanView plan) {
     constexpr int TT = TOK / 4;  // token tiles of 4 (one MFMA's 16 B columns)
+    constexpr int TH = gm_halves(TOK), NWV = GM_WAVES * TH;  // token halves, waves
+    constexpr int TTW = TT / TH;                               // token tiles per wave
     // B fragments of one group: [buffer][window][token tile][64 lanes] x 16 bytes, and the tokens' group factors
     __shared__ u32x4 bl[2][WG][TT][64];
     __shared__ float ex[2][TOK];
@@ -262,12 +267,13 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
         t0 = 0;
         tbase = plan.plan[MOE_PLAN_EXPERTS + blockIdx.y] * tiles;  // the expert's first tile
     }
-    const int tile0 = (blockIdx.x * GM_WAVES + wave) * GM_ROW_TILES;
+    const int wrow = wave % GM_WAVES, jbase = (wave / GM_WAVES) * TTW;  // the wave's rows and first token tile
+    const int tile0 = (blockIdx.x * GM_WAVES + wrow) * GM_ROW_TILES;
     const size_t tile_bytes = (size_t)16 * cols;
 
     // staging of a group's B fragments: piece p = (window, token tile, lane) of the group, 16 bytes each
     constexpr int PIECES = WG * TT * 64;
-    constexpr int PPT = (PIECES + 64 * GM_WAVES - 1) / (64 * GM_WAVES);  // pieces per thread (the last clamped)
+    constexpr int PPT = (PIECES + 64 * NWV - 1) / (64 * NWV);  // pieces per thread (the last clamped)
     struct BStage {
         u32x4 v[PPT];
         float e;
@@ -280,7 +286,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
         g = min(g, groups - 1);
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int p = min((int)threadIdx.x + i * 64 * GM_WAVES, PIECES - 1);
+            const int p = min((int)threadIdx.x + i * 64 * NWV, PIECES - 1);
             const int w = p / (TT * 64), j = (p / 64) % TT, ln = p % 64;
             const int tok = min(t0 + 4 * j + (ln & 15) / 4, tokens - 1);
             const int limb = (ln & 15) % 4;
@@ -292,7 +298,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
     auto b_store = [&](int buf, const BStage &st) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int p = (int)threadIdx.x + i * 64 * GM_WAVES;
+            const int p = (int)threadIdx.x + i * 64 * NWV;
             const int w = p / (TT * 64), j = (p / 64) % TT, ln = p % 64;
             if (p < PIECES) bl[buf][w][j][ln] = st.v[i];
         }
@@ -319,34 +325,34 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
         }
     };
 
-    floatx4 total[GM_ROW_TILES][TT];
+    floatx4 total[GM_ROW_TILES][TTW];
 #pragma unroll
     for (int rt = 0; rt < GM_ROW_TILES; ++rt)
 #pragma unroll
-        for (int j = 0; j < TT; ++j) total[rt][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TTW; ++j) total[rt][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
     // One group: MFMAs with A from registers and B from LDS buffer `buf`, then the group's scaling.
     auto compute = [&](int buf, const AStage &as) {
-        int4v acc[GM_ROW_TILES][TT];
+        int4v acc[GM_ROW_TILES][TTW];
 #pragma unroll
         for (int rt = 0; rt < GM_ROW_TILES; ++rt)
 #pragma unroll
-            for (int j = 0; j < TT; ++j) acc[rt][j] = (int4v){0, 0, 0, 0};
+            for (int j = 0; j < TTW; ++j) acc[rt][j] = (int4v){0, 0, 0, 0};
 #pragma unroll
         for (int w = 0; w < WG; ++w) {
 #pragma unroll
-            for (int j = 0; j < TT; ++j) {
-                const int4v bfrag = __builtin_bit_cast(int4v, bl[buf][w][j][lane]);
+            for (int j = 0; j < TTW; ++j) {
+                const int4v bfrag = __builtin_bit_cast(int4v, bl[buf][w][jbase + j][lane]);
 #pragma unroll
                 for (int rt = 0; rt < GM_ROW_TILES; ++rt)
                     acc[rt][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, as.a[rt][w]), bfrag,
                                                                        acc[rt][j], 0, 0, 0);
             }
         }
-        // lane (q, c): rows 4q..4q+3 of each tile, token 4j + c/4, limb c%4
+        // lane (q, c): rows 4q..4q+3 of each tile, token 4 (jbase + j) + c/4, limb c%4
 #pragma unroll
-        for (int j = 0; j < TT; ++j) {
-            const float tf = ex[buf][4 * j + c / 4];
+        for (int j = 0; j < TTW; ++j) {
+            const float tf = ex[buf][4 * (jbase + j) + c / 4];
 #pragma unroll
             for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
                 const floatx4 f = (floatx4){(float)acc[rt][j][0], (float)acc[rt][j][1], (float)acc[rt][j][2],
@@ -386,7 +392,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
     for (int rt = 0; rt < GM_ROW_TILES; ++rt) {
         const int tile = tile0 + rt;
 #pragma unroll
-        for (int j = 0; j < TT; ++j) {
+        for (int j = 0; j < TTW; ++j) {
             float v[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -395,7 +401,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemm_q8(const uint8_t *__restri
                 x += __shfl_xor(x, 2);
                 v[k] = x;
             }
-            const int tok = t0 + 4 * j + c / 4;
+            const int tok = t0 + 4 * (jbase + j) + c / 4;
             const int row0 = tile * 16 + 4 * q;
             const bool mine = (c & 3) == 0 && tok < tokens && tile < tiles;
             const float r = rsv[min(tok, tokens - 1)];
@@ -478,7 +484,7 @@ static void launch_tok(marin_gpu *g, const marin_quant_matrix *w, const int8_t *
     const int tiles = (int)(w->rows_padded / 16);
     const int rows_per_block = GM_WAVES * GM_ROW_TILES * 16;
     dim3 grid((unsigned)((w->rows_padded + rows_per_block - 1) / rows_per_block), (unsigned)((tokens + TOK - 1) / TOK));
-    gemm_q8<WG, ST, TOK, false><<<grid, dim3(64 * GM_WAVES), 0, g->stream>>>(
+    gemm_q8<WG, ST, TOK, false><<<grid, dim3(64 * GM_WAVES * gm_halves(TOK)), 0, g->stream>>>(
         w->codes, (const ST *)w->scales, limbs, exps, rs, out, (int)tokens, (int)w->rows, (int)w->cols, tiles,
         MoePlanView{});
 }
@@ -488,7 +494,8 @@ static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *li
                      const float *rs, const GemvOut &out, size_t tokens) {
     // a decode batch in one token block of 8; prompts in blocks of 32
     if (tokens <= (size_t)MOE_BATCH) launch_tok<WG, ST, MOE_BATCH>(g, w, limbs, exps, rs, out, tokens);
-    else launch_tok<WG, ST, GM_TOKENS>(g, w, limbs, exps, rs, out, tokens);
+    else if (tokens <= (size_t)GM_TOKENS) launch_tok<WG, ST, GM_TOKENS>(g, w, limbs, exps, rs, out, tokens);
+    else launch_tok<WG, ST, 2 * GM_TOKENS>(g, w, limbs, exps, rs, out, tokens);
 }
 
 void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
