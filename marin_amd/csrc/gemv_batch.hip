@@ -30,9 +30,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BW = 8;      // waves per block
-// items in flight per wave: 8 for one token tile; 6 for two, so two blocks stay resident per compute unit
+// items in flight per wave: 8 for one token tile; 4 for two, so two blocks stay resident per compute unit
+#ifndef BATCH_RING2
+#define BATCH_RING2 4
+#endif
 template <int TT>
-constexpr int bring() { return TT == 1 ? 8 : 6; }
+constexpr int bring() { return TT == 1 ? 8 : BATCH_RING2; }
 constexpr int BATCH_BLOCKS_PER_CU = 2;
 constexpr int OBUF_TILES = 40;  // tiles a block holds outputs for (the grid covers the matrix in as many rounds)
 
