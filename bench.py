@@ -201,6 +201,117 @@ def bench_batch(m, args) -> int:
     return 0
 
 
+def _bf16(a: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bench_linear(m, args) -> int:
+    """Config 1: the isolated quantized linear layer at decode shapes. Weights N(0, 0.02) quantized int8 on the device
+    (int4: random codes, constant scales; the timing does not depend on the values), group 128, f32 scales;
+    activations bf16 N(0, 1) of M tokens, bf16 out. Each case cycles through copies of its matrix totalling more than
+    the 256 MB last-level cache, so every product streams its weights from HBM; `reps` products are one HIP graph
+    replayed between two events. Bytes per product as the survey counts them: N K (1 or 1/2) + N (K / 128) 4 +
+    M K 2 + M N 2. value: the int8 M = 1 cases' bytes over their time."""
+    gpu = m.Gpu()
+    rng = np.random.default_rng(args.seed)
+    shapes = [(4096, 4096), (4096, 12288), (12288, 4096), (4096, 151936)]  # (K, N)
+    cases = []
+    for bits in (8, 4):
+        for K, N in shapes:
+            wbytes = N * K * (1 if bits == 8 else 0.5) + N * (K // 128) * 4
+            copies = max(2, int(np.ceil(300e6 / wbytes)))
+            if bits == 8:
+                mats = [gpu.quantized_synthetic(N, K, 128, args.seed, i) for i in range(copies)]
+            else:
+                codes = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+                scales = np.full(N * (K // 128), 0.01, np.float32)
+                mats = [gpu.upload_quantized(N, K, 4, 128, codes, scales) for _ in range(copies)]
+                del codes
+            for M in (1, 4, 8):
+                x = gpu.typed(m.Dtype.BF16, host=_bf16(rng.standard_normal((M, K))))
+                out = gpu.typed(m.Dtype.BF16, M * N)
+                sec = gpu.time_matmul_bf16(mats, x, M, out, reps=max(2 * copies, 100))
+                nbytes = wbytes + M * K * 2 + M * N * 2
+                cases.append({"bits": bits, "K": K, "N": N, "M": M, "us": round(sec * 1e6, 2),
+                              "GBps": round(nbytes / sec / 1e9, 1), "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4)})
+                print(f"[bench] linear int{bits} K={K} N={N} M={M}: {sec * 1e6:.2f} us, {nbytes / sec / 1e9:.0f} GB/s",
+                      file=sys.stderr, flush=True)
+            del mats
+            gpu.synchronize()
+    one = [c for c in cases if c["bits"] == 8 and c["M"] == 1]
+    tot_b = sum(c["N"] * c["K"] + c["N"] * (c["K"] // 128) * 4 + c["K"] * 2 + c["N"] * 2 for c in one)
+    tot_s = sum(c["us"] for c in one) * 1e-6
+    gbps = tot_b / tot_s / 1e9
+    line = {
+        "metric": "isolated int8/int4 g128 linear, decode shapes, HBM GB/s", "value": round(gbps, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": 100, "warmup": 1, "ms_per_step": round(tot_s / len(one) * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (int8: N(0,0.02) weights quantized on device; int4: random codes; bf16 N(0,1) inputs)",
+        "config": {"workload": "config 1: (K, N) in {(4096,4096), (4096,12288), (12288,4096), (4096,151936)}, "
+                               "M in {1, 4, 8}, int8 and int4 group 128, bf16 in and out; value over int8 M=1"},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "cases": cases,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_paged(m, args) -> int:
+    """Config 2: batched paged GQA decode attention. Batch 16, 32 q / 8 kv heads, head_dim 128, bf16 q/k/v N(0,1),
+    pages of 16 positions; contexts uniform in [512, 8192] (seeded); one pool of exactly the pages needed, dealt to
+    the sequences in a seeded shuffled order; scale 1/sqrt(128), the query at the last position. Bytes per call:
+    sum of contexts x 8 kv heads x 128 x 2 (keys and values) x 2 B, plus q and out. value: bytes / mean call time
+    over `--steps` calls between two events."""
+    gpu = m.Gpu()
+    rng = np.random.default_rng(args.seed)
+    batch, heads, kvh, hd, pt = 16, 32, 8, 128, 16
+    ctx = rng.integers(512, 8193, size=batch).astype(np.uint32)
+    pages_each = [-(-int(c) // pt) for c in ctx]
+    total = sum(pages_each)
+    perm = rng.permutation(total)
+    pool = m.PagePool(gpu, total, pt, kvh, hd, m.KvFormat.BF16)
+    stride = max(pages_each)
+    tables = np.zeros((batch, stride), np.uint32)
+    block = _bf16(rng.standard_normal((64, 2 * pt * kvh * hd)))  # 64 distinct pages of random rows, dealt cyclically
+    at = 0
+    for b in range(batch):
+        for i in range(pages_each[b]):
+            pid = int(perm[at])
+            tables[b, i] = pid
+            pool.write_page(pid, block[at % 64])
+            at += 1
+    q = gpu.typed(m.Dtype.BF16, host=_bf16(rng.standard_normal((batch, heads, hd))))
+    out = gpu.typed(m.Dtype.BF16, batch * heads * hd)
+    for _ in range(5):
+        pool.attention(q, tables, ctx, heads, out)
+    gpu.synchronize()
+    steps = max(args.steps, 20)
+    a = gpu.mark()
+    for _ in range(steps):
+        pool.attention(q, tables, ctx, heads, out)
+    b = gpu.mark()
+    sec = b.since(a) / steps
+    nbytes = int(ctx.sum()) * kvh * hd * 2 * 2 + 2 * batch * heads * hd * 2
+    gbps = nbytes / sec / 1e9
+    print(f"[bench] paged attention batch {batch}: {sec * 1e6:.1f} us per call, {nbytes / 1e6:.1f} MB, {gbps:.0f} GB/s",
+          file=sys.stderr, flush=True)
+    line = {
+        "metric": "batched paged GQA decode attention HBM GB/s (batch 16, ragged contexts)", "value": round(gbps, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": 5, "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (bf16 N(0,1) q/k/v; 64 distinct random pages dealt over the pool)",
+        "config": {"workload": "config 2: batch 16, 32 q / 8 kv heads, head_dim 128, 16-position pages, contexts "
+                               "uniform in [512, 8192], shuffled page tables from one pool", "contexts": ctx.tolist()},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "bytes_per_call": nbytes,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +330,12 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1,
                     help="config 3 at batch N (2..8): N sequences of the prompt length decoded together; one JSON line "
                          "with the aggregate tok/s")
+    ap.add_argument("--linear", action="store_true",
+                    help="config 1 instead: the isolated quantized linear shapes at M 1, 4, 8, int8 and int4, bf16 in "
+                         "and out; one JSON line")
+    ap.add_argument("--paged", action="store_true",
+                    help="config 2 instead: batched paged GQA decode attention, batch 16, ragged contexts; one JSON "
+                         "line")
     ap.add_argument("--moe", action="store_true",
                     help="config 4 instead: the Qwen3-30B-A3B-shaped expert FFN stack at batch 1 and 8 (grouped-expert "
                          "GEMV GB/s), one JSON line")
@@ -244,6 +361,10 @@ def main() -> int:
 
     if args.moe:
         return bench_moe(m, args)
+    if args.linear:
+        return bench_linear(m, args)
+    if args.paged:
+        return bench_paged(m, args)
     if args.batch > 1:
         return bench_batch(m, args)
 

@@ -304,6 +304,12 @@ marin_status marin_moe_stack_time(marin_gpu *gpu, size_t layers, const marin_qua
                                   const marin_buffer *weights, size_t tokens, size_t experts, size_t k,
                                   marin_buffer *act, marin_buffer *out, int part, int reps, double *seconds);
 
+/* Extension (measurement, config 1): `reps` bf16-in/bf16-out products (marin_matmul_quant_bf16) cycling through `n`
+ * same-shaped matrices, captured into one HIP graph and replayed between two events: mean seconds per product. */
+marin_status marin_time_matmul_bf16(marin_gpu *gpu, const marin_quant_matrix *const *mats, size_t n,
+                                    const marin_buffer *x, size_t tokens, marin_buffer *out, int reps,
+                                    double *seconds);
+
 /* Extension (bandwidth probe, the role of cuda/src/probe.rs:145-314): `reps` device-to-device copies of `bytes`
  * (a multiple of 16) through a plain streaming kernel; the mean seconds per copy. */
 marin_status marin_probe_copy(marin_gpu *gpu, size_t bytes, int reps, double *seconds);

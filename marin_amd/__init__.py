@@ -321,6 +321,15 @@ class Gpu:
         check(lib.marin_probe_copy(self._h, nbytes, reps, C.byref(sec)))
         return sec.value
 
+    def time_matmul_bf16(self, mats, x: Buffer, tokens: int, out: Buffer, reps: int = 200) -> float:
+        """Mean seconds per bf16 product over a graph of `reps` products cycling through `mats` (extension; see
+        include/marin_hip.h)."""
+        n = len(mats)
+        arr = (C.c_void_p * n)(*[mm._h.value if hasattr(mm._h, "value") else mm._h for mm in mats])
+        sec = C.c_double()
+        check(lib.marin_time_matmul_bf16(self._h, arr, n, x.handle, tokens, out.handle, reps, C.byref(sec)))
+        return sec.value
+
     # ---- mixture of experts (config 4; see include/marin_hip.h) ----
     def moe_route(self, logits: Buffer, tokens: int, experts: int, k: int, renorm: bool, ids: Buffer,
                   weights: Buffer) -> None:

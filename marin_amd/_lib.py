@@ -124,6 +124,7 @@ SIGNATURES = {
     "marin_qwen3_profile_step": (st, [P, P, C.POINTER(StepProfileC)]),
     "marin_probe_copy": (st, [P, sz, C.c_int, C.POINTER(C.c_double)]),
     "marin_moe_route": (st, [P, P, sz, sz, sz, C.c_int, P, P]),
+    "marin_time_matmul_bf16": (st, [P, P, sz, P, sz, P, C.c_int, C.POINTER(C.c_double)]),
     "marin_moe_ffn": (st, [P, P, P, P, P, C.c_float, P, P, sz, sz, sz, P, P]),
     "marin_moe_stack_time": (st, [P, sz, P, P, P, P, C.c_float, P, P, sz, sz, sz, P, P, C.c_int, C.c_int,
                                   C.POINTER(C.c_double)]),

@@ -456,4 +456,58 @@ marin_status marin_matmul_quant_bf16(marin_gpu *g, const marin_quant_matrix *w, 
     });
 }
 
+// Measurement (config 1): `reps` bf16-in, bf16-out products cycling through `n` same-shaped matrices (so the
+// weights stream from HBM, not the last-level cache), captured into one HIP graph and replayed between two events on
+// the stream: mean seconds per product.
+marin_status marin_time_matmul_bf16(marin_gpu *g, const marin_quant_matrix *const *mats, size_t n,
+                                    const marin_buffer *x, size_t tokens, marin_buffer *out, int reps,
+                                    double *seconds) {
+    return guard([&] {
+        if (!n || reps < 1 || !tokens) shape("timed products", 1, 0);
+        for (size_t i = 0; i < n; ++i) {
+            check_matmul(mats[i], x, tokens, out, MARIN_BF16);
+            if (mats[i]->rows != mats[0]->rows || mats[i]->cols != mats[0]->cols) shape("timed matrix rows", mats[0]->rows, mats[i]->rows);
+            if (!gemv_supported(mats[i])) unsupported("bf16 product layout (group and cols multiples of 64)", 64, mats[i]->group);
+        }
+        auto one = [&](const marin_quant_matrix *w) {
+            GemvIn in;
+            in.mode = IN_BF16;
+            in.x = x->data;
+            in.x_stride = w->cols;
+            GemvOut o;
+            o.mode = OUT_BF16;
+            o.y = out->data;
+            o.y_stride = w->rows;
+            launch_product(g, w, in, o, tokens);
+        };
+        one(mats[0]);  // grows the workspace outside the capture
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        HIP_CHECK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
+        try {
+            for (int r = 0; r < reps; ++r) one(mats[r % n]);
+        } catch (...) {
+            hipGraph_t junk = nullptr;
+            (void)hipStreamEndCapture(g->stream, &junk);
+            if (junk) (void)hipGraphDestroy(junk);
+            throw;
+        }
+        HIP_CHECK(hipStreamEndCapture(g->stream, &graph));
+        hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        hip_check(e, "hipGraphInstantiate");
+        hipEvent_t a = g->next_event(), b = g->next_event();
+        float ms = 0.0f;
+        e = hipGraphLaunch(exec, g->stream);  // warm-up
+        if (e == hipSuccess) e = hipEventRecord(a, g->stream);
+        if (e == hipSuccess) e = hipGraphLaunch(exec, g->stream);
+        if (e == hipSuccess) e = hipEventRecord(b, g->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        (void)hipGraphExecDestroy(exec);
+        hip_check(e, "timed product graph");
+        *seconds = ms * 1e-3 / reps;
+    });
+}
+
 }  // extern "C"
