@@ -150,7 +150,7 @@ constexpr int QR_THREADS = 1024;
 template <int GCOLS, int IT>
 __global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols, int8_t *__restrict__ limbs,
                                                             float *__restrict__ exps, float *__restrict__ rs_out,
-                                                            int ttiles) {
+                                                            int32_t *__restrict__ lsum, int ttiles) {
     constexpr int TPG = GCOLS / 4;
     __shared__ float red[QR_THREADS / 64];
     const int t = blockIdx.x;
@@ -212,9 +212,9 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols,
             sh = 30 - e;
             sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
         }
-        if (!on) continue;
         const float up = ldexpf(1.0f, sh);
         uint32_t word[4] = {0u, 0u, 0u, 0u};
+        int ls[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             int xi = __float2int_rn(x[e] * up);
@@ -222,9 +222,17 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols,
             for (int l = 0; l < 4; ++l) {
                 const int lb = l == 3 ? xi : (int)(int8_t)(xi & 0xff);
                 word[l] |= ((uint32_t)lb & 0xffu) << (8 * e);
+                ls[l] += lb;
                 xi = (xi - lb) >> 8;
             }
         }
+        // the group's sum of each limb (int4 codes are stored + 8: the product removes 8 x this sum exactly)
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+            for (int o = 1; o < TPG; o <<= 1) ls[l] += __shfl_xor(ls[l], o);
+        if (!on) continue;
+        if ((threadIdx.x % TPG) == 0)
+            *reinterpret_cast<int4 *>(lsum + ((size_t)t * groups + k / GCOLS) * 4) = make_int4(ls[0], ls[1], ls[2], ls[3]);
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const int lane = ((k & 63) >> 4) * 16 + (t & 3) * 4 + l;
@@ -531,7 +539,8 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
 static size_t align16(size_t n) { return (n + 15) / 16 * 16; }
 
 size_t moe_gate_up_workspace(size_t tokens, size_t cols, size_t group) {
-    return align16(tokens * 4 * cols) + align16(tokens * (cols / group) * 4) + tokens * 4;
+    return align16(tokens * 4 * cols) + align16(tokens * (cols / group) * 4) + align16(tokens * (cols / group) * 16) +
+           tokens * 4;
 }
 
 ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group, bool frag) {
@@ -542,28 +551,29 @@ ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size
     uint8_t *ws = (uint8_t *)g->workspace(moe_gate_up_workspace(frag ? ttiles * 4 : tokens, cols, group));
     int8_t *limbs = (int8_t *)ws;
     float *exps = (float *)(ws + limb_bytes);
-    float *rs = (float *)(ws + limb_bytes + exp_bytes);
+    int32_t *lsum = (int32_t *)(ws + limb_bytes + exp_bytes);
+    float *rs = (float *)(ws + limb_bytes + exp_bytes + align16(tokens * (cols / group) * 16));
     const unsigned tt = (unsigned)ttiles;
     if (frag && cols <= 4 * 4096) {
         const unsigned nt = (unsigned)tokens;
         const int it = (int)((cols + 4095) / 4096);
         if (group == 128) {
             switch (it) {
-                case 1: quantize_rows<128, 1><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
-                case 2: quantize_rows<128, 2><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
-                case 3: quantize_rows<128, 3><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
-                default: quantize_rows<128, 4><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                case 1: quantize_rows<128, 1><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
+                case 2: quantize_rows<128, 2><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
+                case 3: quantize_rows<128, 3><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
+                default: quantize_rows<128, 4><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
             }
         } else {
             switch (it) {
-                case 1: quantize_rows<64, 1><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
-                case 2: quantize_rows<64, 2><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
-                case 3: quantize_rows<64, 3><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
-                default: quantize_rows<64, 4><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt); break;
+                case 1: quantize_rows<64, 1><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
+                case 2: quantize_rows<64, 2><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
+                case 3: quantize_rows<64, 3><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
+                default: quantize_rows<64, 4><<<nt, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt); break;
             }
         }
         g->launched();
-        return ActLimbs{limbs, exps, rs};
+        return ActLimbs{limbs, exps, rs, lsum};
     }
     if (group == 128) {
         if (frag) quantize_act<128, true><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
@@ -573,7 +583,7 @@ ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size
         else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
     }
     g->launched();
-    return ActLimbs{limbs, exps, rs};
+    return ActLimbs{limbs, exps, rs, nullptr};
 }
 
 template <int WG, typename ST>

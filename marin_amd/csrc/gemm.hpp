@@ -34,6 +34,7 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
 struct ActLimbs {
     const int8_t *limbs;
     const float *exps, *rs;
+    const int32_t *lsum;  // fragment order only: each (token, group)'s four limb sums [tokens][groups][4]
 };
 // With `frag`, the limbs in B-operand fragment order instead ([window][token tile][64 lanes][16 bytes]).
 ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size_t cols, size_t group, bool frag);

@@ -1,5 +1,5 @@
-// The quantized product of a decode batch (2..8 tokens): the one-token product's schedule with the tokens' limbs
-// read from L2.
+// The quantized product of a decode batch (2..8 tokens, int8 or int4 codes): the one-token product's schedule with
+// the tokens' limbs read from L2.
 //
 // Same exact arithmetic as the other products: codes are the A operand of v_mfma_i32_16x16x64_i8, the activations
 // are four signed 8-bit limbs per (token, group) (quantize_act), four tokens x four limbs fill the 16 B columns, so
@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "gemm.hpp"
 
@@ -28,6 +29,7 @@ namespace {
 typedef int int4v __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BW = 8;      // waves per block
 // items in flight per wave: 8 for one token tile; 4 for two, so two blocks stay resident per compute unit
@@ -49,12 +51,15 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 
 }  // namespace
 
+// BITS: 8 or 4 (nibbles stored as code + 8, unpacked to bytes; 8 x the group's limb sums come off the int32 sums);
 // WG: windows per quantization group; TT: token tiles of 4 (1 or 2); SM: windows per wave per tile; ST: scale type.
-template <int WG, int TT, int SM, typename ST>
+template <int BITS, int WG, int TT, int SM, typename ST>
 __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                       const int8_t *__restrict__ limbs,
                                                       const float *__restrict__ exps, const float *__restrict__ rsv,
-                                                      GemvOut out, int tokens, int rows, int cols, int tiles) {
+                                                      const int32_t *__restrict__ lsum, GemvOut out, int tokens,
+                                                      int rows, int cols, int tiles) {
+    constexpr int CB = BITS == 8 ? 16 : 8;  // code bytes per lane per window
     constexpr int S = SM;
     constexpr int BRING = bring<TT>();
     __shared__ __align__(16) float red[2][BW][4 * TT][16];
@@ -67,7 +72,7 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
     const int c = lane & 15, q = lane >> 4;
     const int windows = cols >> 6;
     const int groups = windows / WG;
-    const size_t tile_bytes = (size_t)16 * cols;
+    const size_t tile_bytes = (size_t)16 * (BITS == 8 ? cols : cols / 2);
     const int w0 = wave * S;
     const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int items = my_tiles * S;
@@ -82,23 +87,27 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
     const int ttiles = (tokens + 3) / 4;
     const int8_t *brow[TT];
     const float *erow[TT];
+    const int32_t *orow[TT];
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
         const int tok = min(4 * j + c / 4, tokens - 1);
         const int ln = tok == 4 * j + c / 4 ? lane : 16 * q + 4 * (tok & 3) + (c & 3);
         brow[j] = limbs + ((size_t)(tok >> 2) * 64 + ln) * 16;
         erow[j] = exps + (size_t)tok * groups;
+        orow[j] = BITS == 4 ? lsum + (size_t)tok * groups * 4 + (c & 3) : nullptr;
     }
 
-    u32x4 ra[BRING];
+    typedef typename std::conditional<BITS == 8, u32x4, u32x2>::type Raw;
+    Raw ra[BRING];
     u32x4 rb[BRING][TT];
     floatx4 rs_[BRING / WG];
     float re[BRING / WG][TT];
+    int ro[BRING / WG][TT];
     auto load_item = [&](int i, int slot) {
         const int t = (int)blockIdx.x + (i / S) * (int)gridDim.x;
         const int w = min(w0 + i % S, windows - 1);
         ra[slot] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(codes + (size_t)t * tile_bytes + (size_t)w * 1024 + 16 * lane));
+            reinterpret_cast<const Raw *>(codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane));
 #pragma unroll
         for (int j = 0; j < TT; ++j) rb[slot][j] = *reinterpret_cast<const u32x4 *>(brow[j] + (size_t)w * ttiles * 1024);
         if (slot % WG == WG - 1) {  // the group's factors travel with its last window, read at the group's end
@@ -112,6 +121,10 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
             }
 #pragma unroll
             for (int j = 0; j < TT; ++j) re[slot / WG][j] = erow[j][w / WG];
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int j = 0; j < TT; ++j) ro[slot / WG][j] = 8 * orow[j][(w / WG) * 4];
+            }
         }
     };
     const int last = items > 0 ? items - 1 : 0;
@@ -131,7 +144,14 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
 #pragma unroll
         for (int s = 0; s < BRING; ++s) {
             const int i = base + s;
-            const int4v a = __builtin_bit_cast(int4v, ra[s]);
+            int4v a;
+            if constexpr (BITS == 8) {
+                a = __builtin_bit_cast(int4v, ra[s]);
+            } else {
+                const Raw cur = ra[s];
+                a = (int4v){(int)(cur.x & 0x0f0f0f0fu), (int)((cur.x >> 4) & 0x0f0f0f0fu), (int)(cur.y & 0x0f0f0f0fu),
+                            (int)((cur.y >> 4) & 0x0f0f0f0fu)};
+            }
             int4v b[TT];
 #pragma unroll
             for (int j = 0; j < TT; ++j) b[j] = __builtin_bit_cast(int4v, rb[s][j]);
@@ -148,6 +168,10 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
 #pragma unroll
                 for (int j = 0; j < TT; ++j) {
                     const float gex = re[s / WG][j];
+                    if constexpr (BITS == 4) {
+                        const int off = ro[s / WG][j];
+                        acc[j] -= (int4v){off, off, off, off};
+                    }
                     if (on) {
                         const floatx4 f = (floatx4){(float)acc[j][0], (float)acc[j][1], (float)acc[j][2], (float)acc[j][3]};
                         total[j] += f * (gsc * gex);
@@ -242,47 +266,55 @@ static int batch_slice(int windows) {
 }
 
 bool gemv_batch_supported(const marin_quant_matrix *w, size_t tokens) {
-    return tokens >= 2 && tokens <= 8 && gemm_layout_ok(w) && batch_slice((int)(w->cols / 64)) > 0;
+    return tokens >= 2 && tokens <= 8 && (w->bits == 8 || w->bits == 4) && w->windowed &&
+           (w->group == 64 || w->group == 128) && w->cols % w->group == 0 && batch_slice((int)(w->cols / 64)) > 0;
 }
 
-template <int WG, int TT, int SM, typename ST>
+template <int BITS, int WG, int TT, int SM, typename ST>
 static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
     const int tiles = (int)(w->rows_padded / 16);
-    auto kern = gemv_batch<WG, TT, SM, ST>;
+    auto kern = gemv_batch<BITS, WG, TT, SM, ST>;
     int resident = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * BW, 0) != hipSuccess || resident < 1)
         resident = 1;
     const int blocks = std::max(std::min(tiles, std::min(resident, BATCH_BLOCKS_PER_CU) * std::max(g->cu_count, 1)),
                                 (tiles + OBUF_TILES - 1) / OBUF_TILES);
     kern<<<dim3((unsigned)blocks), dim3(64 * BW), 0, g->stream>>>(w->codes, (const ST *)w->scales, al.limbs, al.exps,
-                                                                   al.rs, out, (int)tokens, (int)w->rows,
+                                                                   al.rs, al.lsum, out, (int)tokens, (int)w->rows,
                                                                    (int)w->cols, tiles);
 }
 
-template <int WG, int TT, typename ST>
+template <int BITS, int WG, int TT, typename ST>
 static void launch_sm(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
     switch (batch_slice((int)(w->cols / 64))) {
-        case 4: launch_t<WG, TT, 4, ST>(g, w, al, out, tokens); break;
-        case 8: launch_t<WG, TT, 8, ST>(g, w, al, out, tokens); break;
-        case 12: launch_t<WG, TT, 12, ST>(g, w, al, out, tokens); break;
-        default: launch_t<WG, TT, 24, ST>(g, w, al, out, tokens); break;
+        case 4: launch_t<BITS, WG, TT, 4, ST>(g, w, al, out, tokens); break;
+        case 8: launch_t<BITS, WG, TT, 8, ST>(g, w, al, out, tokens); break;
+        case 12: launch_t<BITS, WG, TT, 12, ST>(g, w, al, out, tokens); break;
+        default: launch_t<BITS, WG, TT, 24, ST>(g, w, al, out, tokens); break;
+    }
+}
+
+template <int BITS, typename ST>
+static void launch_bits(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out,
+                        size_t tokens) {
+    const bool wg2 = w->group == 128;
+    if (tokens <= 4) {
+        if (wg2) launch_sm<BITS, 2, 1, ST>(g, w, al, out, tokens);
+        else launch_sm<BITS, 1, 1, ST>(g, w, al, out, tokens);
+    } else {
+        if (wg2) launch_sm<BITS, 2, 2, ST>(g, w, al, out, tokens);
+        else launch_sm<BITS, 1, 2, ST>(g, w, al, out, tokens);
     }
 }
 
 template <typename ST>
 static void launch_st(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
-    const bool wg2 = w->group == 128;
-    if (tokens <= 4) {
-        if (wg2) launch_sm<2, 1, ST>(g, w, al, out, tokens);
-        else launch_sm<1, 1, ST>(g, w, al, out, tokens);
-    } else {
-        if (wg2) launch_sm<2, 2, ST>(g, w, al, out, tokens);
-        else launch_sm<1, 2, ST>(g, w, al, out, tokens);
-    }
+    if (w->bits == 8) launch_bits<8, ST>(g, w, al, out, tokens);
+    else launch_bits<4, ST>(g, w, al, out, tokens);
 }
 
 void launch_gemv_batch(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
-    if (!gemv_batch_supported(w, tokens)) unsupported("batch product (2..8 tokens, int8, group 64 or 128)", 8, tokens);
+    if (!gemv_batch_supported(w, tokens)) unsupported("batch product (2..8 tokens, int8 or int4, group 64 or 128)", 8, tokens);
     if (out.argmax && !out.argmax_each) unsupported("batch product greedy choice (one per token only)", 1, 0);
     const ActLimbs al = launch_quantize_act(g, in, tokens, w->cols, w->group, true);
     if (w->bf16_scales) launch_st<uint16_t>(g, w, al, out, tokens);
