@@ -31,6 +31,13 @@ import numpy as np
 HBM_PEAK_GBPS = 8000.0
 
 
+def layer_params(shape: dict) -> int:
+    """Weights of the decoder layers' projections (q, k, v, o, gate, up, down)."""
+    H, F = shape["hidden"], shape["ffn"]
+    qd, kvd = shape["heads"] * shape["head_dim"], shape["kv_heads"] * shape["head_dim"]
+    return shape["layers"] * (H * (qd + 2 * kvd) + qd * H + 3 * F * H)
+
+
 def cpu_baseline(shape: dict, ctx: int, budget_s: float = 12.0) -> dict:
     """Seconds per 8B decode token on one host core: every projection shape of one layer (x36), the output head,
     and attention over `ctx` f32 cached positions for every layer, with the oracle's Q8Gemv and AttendOne."""
@@ -466,6 +473,8 @@ def main() -> int:
         "step_algorithmic_GBps": round((gemv_b + attn_b) / (wall / args.steps) / 1e9, 1),
         "weight_bytes_per_token": weight_bytes(shape),
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
+        # useful int8 work of the prompt's layer products (2 x layer weights x tokens) per second
+        "prefill_int8_TOPs": round(2.0 * layer_params(shape) * args.prompt / prefill_s / 1e12, 1),
         "gpu": info["name"],
         "first_tokens": tokens[:8].tolist(),
     }
