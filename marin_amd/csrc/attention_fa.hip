@@ -6,12 +6,14 @@
 // 22 significant bits); with the fused inputs the token's key gets RMSNorm(k_norm) + RoPE and is stored with its
 // value into the cache, rounded as every cache store.
 //
-// fa_prefill: a workgroup per (16 query tokens, kv head), a wave per q head of the group. Key and value tiles of 32
+// fa_prefill: a workgroup per (16 query tokens, kv head, span of 1024 positions when the context is longer), a wave
+// per q head of the group. Key and value tiles of 32
 // positions are staged in LDS once for the whole group (keys position-major, values transposed), the next tile's
 // loads in flight while the current one is used. Per tile and wave: S = Q K^T on v_mfma_f32_16x16x32_f16 (hi and lo
 // parts: keys are exact in f16, so the scores are f32-grade), causal mask, online softmax in the log2 domain with the
 // row's 2^-s folded into the scale, P through LDS into the A layout split into hi + lo, O += P V on the same MFMA with
-// the transposed values. Rows divide by their running sum at the end.
+// the transposed values. Rows divide by their running sum at the end, or, split over spans, leave the running maximum,
+// sum and values for fa_merge (so no workgroup walks a whole long context alone).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -147,11 +149,15 @@ __global__ __launch_bounds__(576) void fa_prep(const void *__restrict__ qv, Attn
 }
 
 // HD: head size (64 or 128); G: waves = q heads per kv head (1, 2, 4 or 8).
+// span 0: the workgroup walks every visible position and writes the output. span > 0 (a multiple of FA_TILE): split
+// blockIdx.z takes positions [z span, (z + 1) span) and leaves its rows' running maximum, sum and weighted values in
+// `part` ([splits][tokens][heads][HD] values, then [splits][tokens][heads] (max, sum)); fa_merge combines them.
 template <int HD, int G, bool BF16IO>
 __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict__ qh, const _Float16 *__restrict__ ql,
                                                   const float *__restrict__ qe, const uint64_t *__restrict__ table,
                                                   const uint32_t *__restrict__ ctx_lens, KvGeom geom, int tokens,
-                                                  int heads, int kv_heads, float scale, void *__restrict__ out) {
+                                                  int heads, int kv_heads, float scale, int span,
+                                                  float *__restrict__ part, void *__restrict__ out) {
     constexpr int KP = HD + 8;        // key row pitch (halves): rows 16 bytes apart in banks
     constexpr int VP = FA_TILE + 8;   // transposed value row pitch (halves)
     constexpr int CH = HD / 8;        // 16-byte chunks per row
@@ -234,8 +240,10 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         l[i] = 0.0f;
     }
 
-    load_tile(0);
-    for (int p0 = 0; p0 <= max_pos; p0 += FA_TILE) {
+    const int p_begin = span ? (int)blockIdx.z * span : 0;
+    const int p_end = span ? min(p_begin + span, max_pos + 1) : max_pos + 1;  // exclusive
+    load_tile(min(p_begin, max_pos));
+    for (int p0 = p_begin; p0 < p_end; p0 += FA_TILE) {
         __syncthreads();  // every wave is done with the previous tile
         store_tile();
         __syncthreads();
@@ -310,6 +318,22 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         }
         __builtin_amdgcn_wave_barrier();  // reads of pl done before the next tile overwrites it
     }
+    if (span) {
+        // ---- this split's rows: running maximum and sum, unnormalized values (a split past a row's last position
+        // leaves -inf, 0 and zeros)
+        const size_t plane = (size_t)tokens * heads;
+        float *ml = part + (size_t)gridDim.z * plane * HD;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = t0 + 4 * q + i;
+            if (t >= tokens) continue;
+            const size_t unit = (size_t)blockIdx.z * plane + (size_t)t * heads + h;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) part[unit * HD + 16 * d + c] = o[d][i];
+            if (c == 0) *reinterpret_cast<float2 *>(ml + unit * 2) = make_float2(m[i], l[i]);
+        }
+        return;
+    }
     // ---- out: lane holds rows 4 q + i, head value 16 d + c
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -330,7 +354,45 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
     }
 }
 
+// The splits of every (token, head) row combined in split order: weights 2^(m_s - M) of the rows' maxima (log2
+// domain), values summed and divided by the weighted sums. One thread per head value, a workgroup per row.
+template <int HD, bool BF16IO>
+__global__ __launch_bounds__(HD) void fa_merge(const float *__restrict__ part, int splits, int tokens, int heads,
+                                               void *__restrict__ out) {
+    const size_t unit = blockIdx.x, plane = (size_t)tokens * heads;
+    const float *ml = part + (size_t)splits * plane * HD;
+    float mx = -INFINITY;
+    for (int z = 0; z < splits; ++z) mx = fmaxf(mx, ml[((size_t)z * plane + unit) * 2]);
+    float sum = 0.0f, v = 0.0f;
+    for (int z = 0; z < splits; ++z) {
+        const float2 s = *reinterpret_cast<const float2 *>(ml + ((size_t)z * plane + unit) * 2);
+        const float w = s.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s.x - mx);
+        sum += s.y * w;
+        v += part[((size_t)z * plane + unit) * HD + threadIdx.x] * w;
+    }
+    v /= sum;
+    const size_t at = unit * HD + threadIdx.x;
+    if constexpr (BF16IO) {
+        const unsigned u = __float_as_uint(v);
+        reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    } else {
+        reinterpret_cast<float *>(out)[at] = v;
+    }
+}
+
 size_t prefill_fa_scratch(size_t tokens, size_t heads, size_t hd) { return tokens * heads * (hd * 4 + 4); }
+
+constexpr int FA_SPAN = 1024;   // positions per split of a long row
+constexpr int FA_MAX_SPLITS = 8;
+
+// Splits of the rows' positions: one when the context fits a span or the scratch cannot hold the partials.
+static int fa_splits(const AttentionArgs &a) {
+    const size_t hd = a.geom.head_dim;
+    const size_t s = std::min<size_t>((a.max_ctx + FA_SPAN - 1) / FA_SPAN, FA_MAX_SPLITS);
+    if (s <= 1) return 1;
+    const size_t need = (prefill_fa_scratch(a.tokens, a.heads, hd) + 15) / 16 * 16 + s * a.tokens * a.heads * (hd + 2) * 4;
+    return need <= a.partial_floats * 4 ? (int)s : 1;
+}
 
 bool prefill_fa_fits(const AttentionArgs &a) {
     const size_t hd = a.geom.head_dim, group = a.heads / a.kv_heads;
@@ -341,24 +403,31 @@ bool prefill_fa_fits(const AttentionArgs &a) {
 
 template <int HD, int G>
 static void launch_fa_t(marin_gpu *g, const AttentionArgs &a, const _Float16 *qh, const _Float16 *ql, const float *qe,
-                        float scale) {
-    dim3 grid((unsigned)((a.tokens + FA_ROWS - 1) / FA_ROWS), (unsigned)a.kv_heads);
+                        float scale, int splits, float *part) {
+    dim3 grid((unsigned)((a.tokens + FA_ROWS - 1) / FA_ROWS), (unsigned)a.kv_heads, (unsigned)splits);
+    const int span = splits > 1 ? FA_SPAN : 0;
     if (a.bf16_io)
         fa_prefill<HD, G, true><<<grid, 64 * G, 0, g->stream>>>(qh, ql, qe, a.tables, a.ctx, a.geom, (int)a.tokens,
-                                                                (int)a.heads, (int)a.kv_heads, scale, a.out);
+                                                                (int)a.heads, (int)a.kv_heads, scale, span, part, a.out);
     else
         fa_prefill<HD, G, false><<<grid, 64 * G, 0, g->stream>>>(qh, ql, qe, a.tables, a.ctx, a.geom, (int)a.tokens,
-                                                                 (int)a.heads, (int)a.kv_heads, scale, a.out);
+                                                                 (int)a.heads, (int)a.kv_heads, scale, span, part, a.out);
+    if (splits > 1) {
+        g->launched(marin_gpu::ATTENTION, a.bytes_hint, "fa_prefill");
+        const unsigned rows = (unsigned)(a.tokens * a.heads);
+        if (a.bf16_io) fa_merge<HD, true><<<rows, HD, 0, g->stream>>>(part, splits, (int)a.tokens, (int)a.heads, a.out);
+        else fa_merge<HD, false><<<rows, HD, 0, g->stream>>>(part, splits, (int)a.tokens, (int)a.heads, a.out);
+    }
 }
 
 template <int HD>
 static void launch_fa_hd(marin_gpu *g, const AttentionArgs &a, const _Float16 *qh, const _Float16 *ql,
-                         const float *qe, float scale) {
+                         const float *qe, float scale, int splits, float *part) {
     switch (a.heads / a.kv_heads) {
-        case 1: launch_fa_t<HD, 1>(g, a, qh, ql, qe, scale); break;
-        case 2: launch_fa_t<HD, 2>(g, a, qh, ql, qe, scale); break;
-        case 4: launch_fa_t<HD, 4>(g, a, qh, ql, qe, scale); break;
-        default: launch_fa_t<HD, 8>(g, a, qh, ql, qe, scale); break;
+        case 1: launch_fa_t<HD, 1>(g, a, qh, ql, qe, scale, splits, part); break;
+        case 2: launch_fa_t<HD, 2>(g, a, qh, ql, qe, scale, splits, part); break;
+        case 4: launch_fa_t<HD, 4>(g, a, qh, ql, qe, scale, splits, part); break;
+        default: launch_fa_t<HD, 8>(g, a, qh, ql, qe, scale, splits, part); break;
     }
 }
 
@@ -378,9 +447,14 @@ void launch_prefill_fa(marin_gpu *g, const AttentionArgs &a) {
                                                            (int)a.heads, (int)a.kv_heads, qh, ql, qe);
     g->launched();
     const float scale = (float)(1.4426950408889634 / std::sqrt((double)hd));
-    if (hd == 128) launch_fa_hd<128>(g, a, qh, ql, qe, scale);
-    else launch_fa_hd<64>(g, a, qh, ql, qe, scale);
-    g->launched(marin_gpu::ATTENTION, a.bytes_hint, "fa_prefill");
+    // split partials after the q parts
+    const int splits = fa_splits(a);
+    float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.partials) +
+                                            (prefill_fa_scratch(a.tokens, a.heads, hd) + 15) / 16 * 16);
+    if (hd == 128) launch_fa_hd<128>(g, a, qh, ql, qe, scale, splits, part);
+    else launch_fa_hd<64>(g, a, qh, ql, qe, scale, splits, part);
+    if (splits > 1) g->launched(marin_gpu::OTHER, 0.0, "fa_merge");
+    else g->launched(marin_gpu::ATTENTION, a.bytes_hint, "fa_prefill");
 }
 
 }  // namespace marin
