@@ -30,13 +30,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-#ifndef DECODE_WAVES
-#define DECODE_WAVES 8
-#endif
 #ifndef DECODE_RING
 #define DECODE_RING 8
 #endif
-constexpr int DW = DECODE_WAVES;   // waves per block
 constexpr int RING = DECODE_RING;  // code windows in flight per wave
 #ifndef DECODE_BPC
 #define DECODE_BPC 2
@@ -87,12 +83,13 @@ __device__ unsigned long long decode_trace[4096 * 8];
 
 // BITS 8 or 4; WG = 64-column windows per quantization group (group = 64 * WG); SM = windows per wave per tile
 // (wave w owns windows [w * SM, (w + 1) * SM) of every row; waves past the last window hold no groups); ST = scale
-// type (float or bf16 bits).
+// type (float or bf16 bits); DW = waves per block (4 for rows of at most 32 windows, where 8 waves would get only a
+// few windows of each tile, else 8).
 //
 // Every global load is unconditional (out-of-range addresses are clamped), and the activation loads are issued
 // before the code ring: the memory counter the wave waits on then lets the activations arrive without draining the
 // ring, and the ring stays exactly RING windows deep through the main loop.
-template <int BITS, int WG, int SM, typename ST>
+template <int BITS, int WG, int SM, typename ST, int DW>
 __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                        GemvIn in, GemvOut out, int rows, int cols, int tiles) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -125,20 +122,22 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     const int *map_p = in.tile_map ? in.tile_map : reinterpret_cast<const int *>(in.x);
     const int map_v = map_p[min(lane, max(in.map_count, 1) - 1)];
 
-    // ---- the activations, block-wide: in round r, thread T holds the 16 consecutive columns 8192 r + 16 T .. + 16,
-    // i.e. quarter T % 4 of window 128 r + T / 4: exactly what the B operand of that window needs, so the thread
-    // builds all four limbs of its columns and stores each as 16 bytes; every wave then reads the limbs of its own
+    // ---- the activations, block-wide: in round r, thread T holds the 16 consecutive columns RC r + 16 T .. + 16
+    // (RC = 1024 DW columns per round), i.e. quarter T % 4 of window 16 DW r + T / 4: exactly what the B operand of
+    // that window needs, so the thread builds all four limbs of its columns and stores each as 16 bytes; every wave
+    // then reads the limbs of its own
     // windows. Each column is loaded once per block; threads past the row's end all load the row's last 16 columns
     // (one cache line per wave). Four 16-byte loads per round (bf16 rows use the first two) and the norm weights
     // (the activation address stands in when there is no norm), all unconditional and issued before the code ring:
     // with no branch around them the waits for them are exact and never drain the ring.
-    constexpr int R = (S + 15) / 16;  // rounds of 8192 columns: DW * S windows at most
+    constexpr int RC = 1024 * DW;     // columns per round
+    constexpr int R = (S + 15) / 16;  // rounds: DW * S windows at most, 16 DW per round
     const bool norm = in.mode == IN_NORM, bf = in.mode == IN_BF16;
     const unsigned char *xb = reinterpret_cast<const unsigned char *>(in.x);
     u32x4 xr[R][4], nr[R][4];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int cb = min(r * 8192 + 16 * (int)threadIdx.x, cols - 16);
+        const int cb = min(r * RC + 16 * (int)threadIdx.x, cols - 16);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const size_t xo = bf ? (size_t)cb * 2 + 16 * (v & 1) : (size_t)cb * 4 + 16 * v;
@@ -183,7 +182,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         }
     }
     auto in_row = [&](int r) {  // this thread's columns lie in the row
-        return r * 8192 + 16 * (int)threadIdx.x < cols;
+        return r * RC + 16 * (int)threadIdx.x < cols;
     };
     // the RMSNorm statistic: the waves' partial sums meet at the prologue's barrier; the limbs hold x * weight, and
     // the factor 1 / sqrt(mean(x^2) + eps) multiplies each row's sum at the end, so no barrier waits for it here
@@ -199,8 +198,8 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        if (r * 8192 + wave * 1024 >= cols) continue;  // wave-uniform: nothing loaded
-        const int wr = r * 128 + (int)threadIdx.x / 4;  // window of this thread's columns
+        if (r * RC + wave * 1024 >= cols) continue;  // wave-uniform: nothing loaded
+        const int wr = r * 16 * DW + (int)threadIdx.x / 4;  // window of this thread's columns
         const bool valid = in_row(r);
         float v[16];
         float mx = 0.0f;
@@ -366,19 +365,27 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     }
 }
 
-// Windows per wave per tile for a row of `windows` 64-column windows: the smallest instantiated width whose DW
-// slices cover the row, 0 when none does.
-static int slice_windows(int windows) {
-    for (int sm : {4, 8, 24})
-        if (DW * sm >= windows) return sm;
+// Waves per block and windows per wave per tile for a row of `windows` 64-column windows: 4 waves for rows of at most
+// 32 windows, else 8; the smallest instantiated width whose slices cover the row. 0 when none does.
+static int slice_windows(int windows, int &dw) {
+    dw = windows <= 32 ? 4 : 8;
+    const int widths4[] = {4, 8}, widths8[] = {8, 12, 24};
+    if (dw == 4) {
+        for (int sm : widths4)
+            if (4 * sm >= windows) return sm;
+    } else {
+        for (int sm : widths8)
+            if (8 * sm >= windows) return sm;
+    }
     return 0;
 }
 
-template <int BITS, int WG, int SM, typename ST>
+template <int BITS, int WG, int SM, typename ST, int DW>
 static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
     // the instantiation's name as rocprof prints it, for the launch profile
     static const std::string name = "gemv_decode<" + std::to_string(BITS) + ", " + std::to_string(WG) + ", " +
-                                    std::to_string(SM) + ", " + (sizeof(ST) == 4 ? "float" : "unsigned short") + ">";
+                                    std::to_string(SM) + ", " + (sizeof(ST) == 4 ? "float" : "unsigned short") + ", " +
+                                    std::to_string(DW) + ">";
     const int windows = (int)(w->cols / 64);
     const int groups = windows / WG;
     // a tile map makes the product's (logical) tiles the mapped blocks of tiles
@@ -388,7 +395,7 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     const int rows = in.tile_map ? tiles * 16 : (int)w->rows;
     const size_t gpad = (size_t)((groups + 3) & ~3);
     const size_t lds = (size_t)DW * SM * 256 + gpad * 4 + (BITS == 4 ? gpad * 16 : 0) + (size_t)(2 * DW * 16 + DW) * 4;
-    auto kern = gemv_decode<BITS, WG, SM, ST>;
+    auto kern = gemv_decode<BITS, WG, SM, ST, DW>;
     if (lds > 64 * 1024) {
         if (lds > 160 * 1024) unsupported("decode product shared memory (KiB)", 160, lds / 1024);
         HIP_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -415,11 +422,15 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
 
 template <int BITS, int WG, typename ST>
 static const char *launch_decode_sm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
-    switch (slice_windows((int)(w->cols / 64))) {
-        case 4: return launch_decode_t<BITS, WG, 4, ST>(g, w, in, out);
-        case 8: return launch_decode_t<BITS, WG, 8, ST>(g, w, in, out);
-        default: return launch_decode_t<BITS, WG, 24, ST>(g, w, in, out);
+    int dw = 0;
+    const int sm = slice_windows((int)(w->cols / 64), dw);
+    if (dw == 4) {
+        if (sm == 4) return launch_decode_t<BITS, WG, 4, ST, 4>(g, w, in, out);
+        return launch_decode_t<BITS, WG, 8, ST, 4>(g, w, in, out);
     }
+    if (sm == 8) return launch_decode_t<BITS, WG, 8, ST, 8>(g, w, in, out);
+    if (sm == 12) return launch_decode_t<BITS, WG, 12, ST, 8>(g, w, in, out);
+    return launch_decode_t<BITS, WG, 24, ST, 8>(g, w, in, out);
 }
 
 template <typename ST>
@@ -430,7 +441,8 @@ static const char *launch_decode_st(marin_gpu *g, const marin_quant_matrix *w, c
 }
 
 bool gemv_decode_supported(const marin_quant_matrix *w) {
-    return gemv_supported(w) && (w->group == 64 || w->group == 128) && slice_windows((int)(w->cols / 64)) > 0;
+    int dw = 0;
+    return gemv_supported(w) && (w->group == 64 || w->group == 128) && slice_windows((int)(w->cols / 64), dw) > 0;
 }
 
 #ifdef DECODE_TRACE
