@@ -152,16 +152,21 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     typedef typename std::conditional<BITS == 8, u32x4, u32x2>::type Raw;
     Raw ring[RING];
     floatx4 sring[RING / WG];
-    auto load_item = [&](int i, int slot) {
-        const int tl = (int)blockIdx.x + (i / S) * (int)gridDim.x;  // logical tile
-        const int t = in.tile_map ? __builtin_amdgcn_readlane(map_v, tl / in.map_tiles) * in.map_tiles + tl % in.map_tiles
-                                  : tl;
-        const int w = min(w0 + i % S, windows - 1);
+    auto tile_of = [&](int tl) {  // logical tile -> tile of the matrix
+        return in.tile_map ? __builtin_amdgcn_readlane(map_v, tl / in.map_tiles) * in.map_tiles + tl % in.map_tiles : tl;
+    };
+    auto load_at = [&](int t, int w, int slot) {  // window w (clamped to the row) of tile t into ring slot `slot`
         const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane;
         if constexpr (BITS == 8) ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
         else ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
         if (slot % WG == 0) sring[slot / WG] = scales4(scales + ((size_t)t * groups + w / WG) * 16 + 4 * q);
     };
+    auto load_item = [&](int i, int slot) {
+        load_at(tile_of((int)blockIdx.x + (i / S) * (int)gridDim.x), min(w0 + i % S, windows - 1), slot);
+    };
+    // Slices a whole number of ring rounds long: a round's items are windows bw .. bw + RING - 1 of one tile, so the
+    // tile (with its map lookup) and the item bounds are worked out once per round, not per window.
+    constexpr bool ALIGNED = S % RING == 0;
     const int last = items > 0 ? items - 1 : 0;
 #pragma unroll
     for (int j = 0; j < RING; ++j) load_item(min(j, last), j);
@@ -273,14 +278,30 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     unsigned long long best = 0ull;
     int tile_n = 0;
     for (int base = 0; base < items; base += RING) {
+        // ALIGNED: the next round's tile and first window; past the last item every refill loads this round's last
+        // window again (one cache line per lane group, so the refills stay unconditional without re-reading the
+        // round). items is a multiple of RING, so every item of a round is real.
+        int nt = 0, nw = 0, ns = 1;
+        if constexpr (ALIGNED) {
+            const bool past = base + RING > last;
+            const int nb = past ? base : base + RING;
+            nt = tile_of((int)blockIdx.x + (nb / S) * (int)gridDim.x);
+            nw = w0 + nb % S + (past ? RING - 1 : 0);
+            ns = past ? 0 : 1;
+        }
+        const int bw = ALIGNED ? base % S : 0;
 #pragma unroll
         for (int j = 0; j < RING; ++j) {
             const int i = base + j;
             const Raw cur = ring[j];
             if (j % WG == 0) gsc = sring[j / WG];  // the slot is refilled below, before the group's last window
-            load_item(min(i + RING, last), j);
-            if (i >= items) continue;
-            const int wl = i % S;      // window inside the slice
+            if constexpr (ALIGNED) {
+                load_at(nt, min(nw + ns * j, windows - 1), j);
+            } else {
+                load_item(min(i + RING, last), j);
+                if (i >= items) continue;
+            }
+            const int wl = ALIGNED ? bw + j : i % S;  // window inside the slice
             const int w = w0 + wl;     // window of the row
             int4v b = (int4v){0, 0, 0, 0};
             if (c < 4 && w < windows) b = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + c) * 64 + 16 * q);
