@@ -164,12 +164,17 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     auto load_item = [&](int i, int slot) {
         load_at(tile_of((int)blockIdx.x + (i / S) * (int)gridDim.x), min(w0 + i % S, windows - 1), slot);
     };
-    // Slices a whole number of ring rounds long: a round's items are windows bw .. bw + RING - 1 of one tile, so the
-    // tile (with its map lookup) and the item bounds are worked out once per round, not per window.
+    // The refills' tiles (with their map lookups) are worked out once per ring round, not per window. Slices a whole
+    // number of rounds long (ALIGNED): a round's items are windows bw .. bw + RING - 1 of one tile. Otherwise a round's
+    // items run over at most NQ consecutive tiles, each item's tile picked with compile-time bounds.
     constexpr bool ALIGNED = S % RING == 0;
+    constexpr int NQ = (S + RING - 1) / S + 1;
+    static_assert(NQ <= 3, "a ring round spans at most three tiles");
     const int last = items > 0 ? items - 1 : 0;
 #pragma unroll
     for (int j = 0; j < RING; ++j) load_item(min(j, last), j);
+    const int t_last = tile_of((int)blockIdx.x + (last / S) * (int)gridDim.x);  // refills past the last item
+    const int w_last = min(w0 + last % S, windows - 1);
     TRACE(2);
 
     // ---- prologue: the limbs (and the RMSNorm partial sums: the threads' columns cover the row once)
@@ -290,6 +295,14 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             ns = past ? 0 : 1;
         }
         const int bw = ALIGNED ? base % S : 0;
+        int q0 = 0, r0 = 0, tq[3] = {0, 0, 0};
+        if constexpr (!ALIGNED) {
+            const int nb = base + RING;
+            q0 = nb / S;
+            r0 = nb % S;
+#pragma unroll
+            for (int d = 0; d < NQ; ++d) tq[d] = tile_of((int)blockIdx.x + (q0 + d) * (int)gridDim.x);
+        }
 #pragma unroll
         for (int j = 0; j < RING; ++j) {
             const int i = base + j;
@@ -298,7 +311,11 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             if constexpr (ALIGNED) {
                 load_at(nt, min(nw + ns * j, windows - 1), j);
             } else {
-                load_item(min(i + RING, last), j);
+                const int off = r0 + j;  // window of the refill counted from tile q0's first
+                const int d = off >= 2 * S ? 2 : (off >= S ? 1 : 0);
+                const bool past = i + RING > last;
+                load_at(past ? t_last : (d == 0 ? tq[0] : d == 1 ? tq[1] : tq[2]),
+                        past ? w_last : min(w0 + off - d * S, windows - 1), j);
                 if (i >= items) continue;
             }
             const int wl = ALIGNED ? bw + j : i % S;  // window inside the slice
