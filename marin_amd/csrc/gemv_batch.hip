@@ -103,9 +103,7 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
     floatx4 rs_[BRING / WG];
     float re[BRING / WG][TT];
     int ro[BRING / WG][TT];
-    auto load_item = [&](int i, int slot) {
-        const int t = (int)blockIdx.x + (i / S) * (int)gridDim.x;
-        const int w = min(w0 + i % S, windows - 1);
+    auto load_at = [&](int t, int w, int slot) {  // window w (clamped to the row) of tile t into ring slot `slot`
         ra[slot] = __builtin_nontemporal_load(
             reinterpret_cast<const Raw *>(codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane));
 #pragma unroll
@@ -127,6 +125,12 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
             }
         }
     };
+    auto load_item = [&](int i, int slot) {
+        load_at((int)blockIdx.x + (i / S) * (int)gridDim.x, min(w0 + i % S, windows - 1), slot);
+    };
+    // Slices a whole number of ring rounds long (ALIGNED): a round's refills are windows of one tile, worked out once
+    // per round; past the last item every refill loads this round's last window again.
+    constexpr bool ALIGNED = S % BRING == 0;
     const int last = items > 0 ? items - 1 : 0;
 #pragma unroll
     for (int j = 0; j < BRING; ++j) load_item(min(j, last), j);
@@ -141,6 +145,14 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
     int tile_n = 0;
     const float lw = (c & 3) == 0 ? 1.0f : (c & 3) == 1 ? 256.0f : (c & 3) == 2 ? 65536.0f : 16777216.0f;
     for (int base = 0; base < items; base += BRING) {
+        int nt = 0, nw = 0, ns = 1;
+        if constexpr (ALIGNED) {
+            const bool past = base + BRING > last;
+            const int nb = past ? base : base + BRING;
+            nt = (int)blockIdx.x + (nb / S) * (int)gridDim.x;
+            nw = w0 + nb % S + (past ? BRING - 1 : 0);
+            ns = past ? 0 : 1;
+        }
 #pragma unroll
         for (int s = 0; s < BRING; ++s) {
             const int i = base + s;
@@ -155,9 +167,10 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
             int4v b[TT];
 #pragma unroll
             for (int j = 0; j < TT; ++j) b[j] = __builtin_bit_cast(int4v, rb[s][j]);
-            // items past the block's last one (the ring's tail) contribute zeros and end no tile
-            const bool valid = i < items;
-            const int wl = i % S;
+            // items past the block's last one (the ring's tail) contribute zeros and end no tile; with ALIGNED slices
+            // items is a multiple of the ring, so there are none
+            const bool valid = ALIGNED || i < items;
+            const int wl = ALIGNED ? base % S + s : i % S;
             const int w = w0 + wl;
             const bool on = valid && w < windows;
 #pragma unroll
@@ -214,7 +227,8 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
             }
             // the slot is refilled once everything in it is consumed, so its registers carry straight over to the
             // next round
-            load_item(min(i + BRING, last), s);
+            if constexpr (ALIGNED) load_at(nt, min(nw + ns * s, windows - 1), s);
+            else load_item(min(i + BRING, last), s);
         }
     }
     __syncthreads();
