@@ -206,10 +206,19 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
         if (lane == 0) ssq[wave] = ss;
     }
+    // windows past the row's end (up to the slices' DW * S) get zero limbs, so the main loop reads every window's
+    // limbs unconditionally and those windows add nothing
+    const u32x4 zero4 = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        if (r * RC + wave * 1024 >= cols) continue;  // wave-uniform: nothing loaded
         const int wr = r * 16 * DW + (int)threadIdx.x / 4;  // window of this thread's columns
+        if (r * RC + wave * 1024 >= cols) {  // wave-uniform: nothing loaded
+            if (wr < DW * S) {
+#pragma unroll
+                for (int l = 0; l < 4; ++l) *reinterpret_cast<u32x4 *>(limbs + ((size_t)wr * 4 + l) * 64 + 16 * (lane & 3)) = zero4;
+            }
+            continue;
+        }
         const bool valid = in_row(r);
         float v[16];
         float mx = 0.0f;
@@ -247,10 +256,10 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
                 xi = (xi - lb) >> 8;
             }
         }
-        if (valid) {
+        if (wr < DW * S) {
 #pragma unroll
             for (int l = 0; l < 4; ++l)
-                *reinterpret_cast<u32x4 *>(limbs + ((size_t)wr * 4 + l) * 64 + 16 * (lane & 3)) = pk[l];
+                *reinterpret_cast<u32x4 *>(limbs + ((size_t)wr * 4 + l) * 64 + 16 * (lane & 3)) = valid ? pk[l] : zero4;
         }
         const int g = wr / WG;
         if (valid && (lane & (4 * WG - 1)) == 0) gdown[g] = ldexpf(1.0f, -sh);
@@ -320,8 +329,8 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             }
             const int wl = ALIGNED ? bw + j : i % S;  // window inside the slice
             const int w = w0 + wl;     // window of the row
-            int4v b = (int4v){0, 0, 0, 0};
-            if (c < 4 && w < windows) b = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + c) * 64 + 16 * q);
+            // lanes c >= 4 (B columns 4..15, whose sums are never used) read the limbs of lane c % 4
+            const int4v b = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + (c & 3)) * 64 + 16 * q);
             int4v a;
             if constexpr (BITS == 8) {
                 a = __builtin_bit_cast(int4v, cur);
@@ -332,16 +341,15 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
             if (j % WG == WG - 1) {
                 // end of a group: one conversion, scaled by weight scale x 2^-shift of the group
-                if (w < windows) {
-                    const int g = w / WG;
-                    if constexpr (BITS == 4) {
-                        const int off = c < 4 ? goff[g * 4 + c] : 0;
-                        acc -= (int4v){off, off, off, off};
-                    }
-                    const float d = gdown[g];
-                    const floatx4 f = (floatx4){(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
-                    total += f * (gsc * d);
+                // past the row's end the sums are zero and any finite factor will do
+                const int g = min(w / WG, groups - 1);
+                if constexpr (BITS == 4) {
+                    const int off = c < 4 && w < windows ? goff[g * 4 + c] : 0;
+                    acc -= (int4v){off, off, off, off};
                 }
+                const float d = gdown[g];
+                const floatx4 f = (floatx4){(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
+                total += f * (gsc * d);
                 acc = (int4v){0, 0, 0, 0};
             }
             if (wl == S - 1) {
