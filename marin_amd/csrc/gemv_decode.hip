@@ -38,6 +38,9 @@ constexpr int RING = DECODE_RING;  // code windows in flight per wave
 #define DECODE_BPC 2
 #endif
 constexpr int DECODE_BLOCKS_PER_CU = DECODE_BPC;
+#ifndef DECODE_HALF
+#define DECODE_HALF 1
+#endif
 constexpr int MAP_MAX = 64;  // tile map entries (selected experts) a launch may carry: one per lane  // resident blocks the persistent grid aims at per compute unit
 
 // Lane permutations inside rows of 16 lanes (DPP): 0xB1 swaps neighbours, 0x4E swaps pairs, 0x141 mirrors each
@@ -91,7 +94,8 @@ __device__ unsigned long long decode_trace[4096 * 8];
 // ring, and the ring stays exactly RING windows deep through the main loop.
 template <int BITS, int WG, int SM, typename ST, int DW>
 __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
-                                                       GemvIn in, GemvOut out, int rows, int cols, int tiles) {
+                                                       GemvIn in, GemvOut out, int rows, int cols, int tiles,
+                                                       int half) {
     extern __shared__ __align__(16) unsigned char lds[];
     TRACE(0);
     constexpr int S = SM;
@@ -152,14 +156,23 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     typedef typename std::conditional<BITS == 8, u32x4, u32x2>::type Raw;
     Raw ring[RING];
     floatx4 sring[RING / WG];
-    auto tile_of = [&](int tl) {  // logical tile -> tile of the matrix
-        return in.tile_map ? __builtin_amdgcn_readlane(map_v, tl / in.map_tiles) * in.map_tiles + tl % in.map_tiles : tl;
+    // Half tiles (half = 1): logical tile tl is rows 8 (tl % 2) .. + 7 of tile tl / 2 over all its columns; the lanes
+    // of the other 8 rows load their partner's row (the same cache lines), so the MFMA's rows 8..15 repeat rows 0..7
+    // and are dropped at the end. A tile code is (tile of the matrix << half) | half-tile bit.
+    auto tile_of = [&](int tl) {  // logical tile -> tile code
+        const int pl = tl >> half;
+        const int t = in.tile_map ? __builtin_amdgcn_readlane(map_v, pl / in.map_tiles) * in.map_tiles + pl % in.map_tiles
+                                  : pl;
+        return (t << half) | (tl & half);
     };
-    auto load_at = [&](int t, int w, int slot) {  // window w (clamped to the row) of tile t into ring slot `slot`
-        const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane;
+    auto load_at = [&](int tc, int w, int slot) {  // window w (clamped to the row) of tile code tc into ring slot `slot`
+        const int t = tc >> half, hb = tc & half;
+        const int la = half ? (c & 7) + 8 * hb + 16 * q : lane;  // the lane whose 16 bytes this lane loads
+        const int qs = half ? (q & 1) + 2 * hb : q;               // the rows 4 qs .. + 3 whose scales it takes
+        const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * la;
         if constexpr (BITS == 8) ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
         else ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
-        if (slot % WG == 0) sring[slot / WG] = scales4(scales + ((size_t)t * groups + w / WG) * 16 + 4 * q);
+        if (slot % WG == 0) sring[slot / WG] = scales4(scales + ((size_t)t * groups + w / WG) * 16 + 4 * qs);
     };
     auto load_item = [&](int i, int slot) {
         load_at(tile_of((int)blockIdx.x + (i / S) * (int)gridDim.x), min(w0 + i % S, windows - 1), slot);
@@ -374,12 +387,14 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
                     for (int ww = 0; ww < DW; ++ww) v += rb[ww * 16 + lane];
                     v *= rs;
                     const int t = (int)blockIdx.x + tile_n * (int)gridDim.x;
-                    const int row = t * 16 + lane;
+                    // half tiles: lanes 0..7 hold rows 8 (t % 2) .. of tile t / 2
+                    const int row = half ? (t >> 1) * 16 + 8 * (t & 1) + lane : t * 16 + lane;
+                    const bool mine = row < rows && (!half || lane < 8);
                     if (out.mode == OUT_SILU) {
                         const float upv = __shfl_xor(v, 1);
-                        if ((lane & 1) == 0 && row < rows)
+                        if ((lane & 1) == 0 && mine)
                             reinterpret_cast<float *>(out.y)[row >> 1] = silu_f(v) * upv;
-                    } else if (row < rows) {
+                    } else if (mine) {
                         if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[row] = v;
                         else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[row] += v;
                         else {
@@ -450,7 +465,13 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * DW, lds) != hipSuccess || resident < 1)
         resident = 1;
     const int cu = std::max(g->cu_count, 1);
-    const int blocks = std::min(tiles, std::min(resident, DECODE_BLOCKS_PER_CU) * cu);
+    // Half tiles where whole tiles load the compute units unevenly and the busiest unit's bytes drop by a fifth or
+    // more: 384 tiles on 256 units put 2 tiles on half of them, 768 half tiles put 3 halves on each. A half tile
+    // costs a whole tile's instructions for half its bytes, so nowhere else.
+    const int full_load = (tiles + cu - 1) / cu, half_load2 = (2 * tiles + cu - 1) / cu;  // (half tiles: x 2)
+    const int half = DECODE_HALF && !in.tile_map && 5 * half_load2 <= 8 * full_load ? 1 : 0;
+    const int items = tiles << half;
+    const int blocks = std::min(items, std::min(resident, DECODE_BLOCKS_PER_CU) * cu);
     if (g->only && name != g->only) {
         g->skipped = true;
         return name.c_str();
@@ -459,10 +480,10 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     g->kernel_events(t0, t1);
     if (t0)
         hipExtLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * DW), (uint32_t)lds, g->stream, t0, t1, 0u, w->codes,
-                              (const ST *)w->scales, in, out, rows, (int)w->cols, tiles);
+                              (const ST *)w->scales, in, out, rows, (int)w->cols, items, half);
     else
         kern<<<dim3((unsigned)blocks), dim3(64 * DW), lds, g->stream>>>(w->codes, (const ST *)w->scales, in, out,
-                                                                        rows, (int)w->cols, tiles);
+                                                                        rows, (int)w->cols, items, half);
     return name.c_str();
 }
 
