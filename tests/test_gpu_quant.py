@@ -114,6 +114,23 @@ def test_int8_embedding_lookup_is_bit_exact_and_refuses_what_it_cannot_do(gpu): 
         gpu.embed_quant(narrow, [1], ids, one)
 
 
+# one token, f32 scales and activations, the a5 tolerance, at the shapes whose tile counts select half tiles (the 8B
+# qkv: 384 tiles on 256 compute units, and one row short of it; the 1.7B down: 128 tiles of 96 windows, slices that
+# are not whole ring rounds) and at whole-tile shapes beside them
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("rows,cols", [(6144, 4096), (6143, 4096), (2048, 6144), (4096, 4096), (3072, 2048)])
+def test_one_token_products_at_half_and_whole_tile_shapes(gpu, bits, rows, cols):
+    print(f"case bits={bits} {rows}x{cols}", flush=True)
+    weights = o.bf16_bits(values_fast(rows * cols, 21) * np.float32(0.05))
+    codes, scales = o.quantize(weights, rows, cols, bits, 128)
+    x = values_fast(cols, 78)
+    expected = reference_matmul(codes, scales, rows, cols, bits, 128, x, 1)
+    w = gpu.upload_quantized(rows, cols, bits, 128, codes, scales)
+    out = gpu.zeros(rows)
+    gpu.matmul_quant(w, gpu.upload(x), 1, out)
+    assert_close(gpu.download(out), expected, 1e-4)
+
+
 @pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 12288), (12288, 4096), (4096, 151936)])
 @pytest.mark.parametrize("m_tokens", [1, 4, 8])
 def test_decode_shapes_bf16_layout_within_the_north_star_tolerance(gpu, k, n, m_tokens):
