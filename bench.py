@@ -218,7 +218,7 @@ def bench_linear(m, args) -> int:
     (int4: random codes, constant scales; the timing does not depend on the values), group 128, f32 scales;
     activations bf16 N(0, 1) of M tokens, bf16 out. Each case cycles through copies of its matrix totalling more than
     the 256 MB last-level cache, so every product streams its weights from HBM; `reps` products are one HIP graph
-    replayed between two events. Bytes per product as the survey counts them: N K (1 or 1/2) + N (K / 128) 4 +
+    replayed between two events. Bytes per product: N K (1 or 1/2) + N (K / 128) 4 +
     M K 2 + M N 2. value: the int8 M = 1 cases' bytes over their time."""
     gpu = m.Gpu()
     rng = np.random.default_rng(args.seed)
