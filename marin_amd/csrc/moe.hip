@@ -139,20 +139,28 @@ __global__ __launch_bounds__(64) void moe_plan(const int32_t *__restrict__ ids, 
 
 // grid: (H / 16 output tiles, tokens); a wave per expert slot j < k. WG: 64-column windows per group; MW: windows of
 // an expert's input (F / 64, at most 16) rounded up to what the template holds.
+#ifndef MOE_DOWN_HALF
+#define MOE_DOWN_HALF 1
+#endif
+
 template <int WG, int MW, typename ST>
 __global__ __launch_bounds__(64 * MOE_MAX_K) void expert_down(const uint8_t *__restrict__ codes,
                                                               const ST *__restrict__ scales,
                                                               const float *__restrict__ act,
                                                               const int32_t *__restrict__ ids,
                                                               const float *__restrict__ weights, int k, int hidden,
-                                                              int ffn, float *__restrict__ out) {
+                                                              int ffn, float *__restrict__ out, int half) {
     __shared__ __align__(16) int8_t limbs[MOE_MAX_K][MW][4][64];
     __shared__ float gdown[MOE_MAX_K][MW];
     __shared__ float red[MOE_MAX_K][16];
     const int lane = threadIdx.x & 63;
     const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q = lane >> 4;
-    const int b = blockIdx.y, tile = blockIdx.x;
+    // half tiles (half = 1): workgroup x takes rows 8 (x % 2) .. + 7 of tile x / 2; the lanes of the other 8 rows
+    // load their partner's row, so the MFMA's rows 8..15 repeat rows 0..7 and are dropped
+    const int b = blockIdx.y, tile = (int)blockIdx.x >> half, hb = (int)blockIdx.x & half;
+    const int la = half ? (c & 7) + 8 * hb + 16 * q : lane;  // the lane whose 16 code bytes this lane loads
+    const int qs = half ? (q & 1) + 2 * hb : q;               // the rows 4 qs .. + 3 whose scales it takes
     const int windows = ffn >> 6, groups = windows / WG;
     const int tiles_per_expert = hidden / 16;
     const bool on = slot < k;
@@ -169,9 +177,9 @@ __global__ __launch_bounds__(64 * MOE_MAX_K) void expert_down(const uint8_t *__r
 #pragma unroll
     for (int w = 0; w < MW; ++w) {
         const int wc = min(w, windows - 1);
-        a[w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(codes + ptile * 16 * ffn + (size_t)wc * 1024 + 16 * lane));
+        a[w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(codes + ptile * 16 * ffn + (size_t)wc * 1024 + 16 * la));
         if (w % WG == 0) {
-            const ST *sp = scales + (ptile * groups + wc / WG) * 16 + 4 * q;
+            const ST *sp = scales + (ptile * groups + wc / WG) * 16 + 4 * qs;
             if constexpr (sizeof(ST) == 4) {
                 sc[w / WG] = *reinterpret_cast<const floatx4 *>(sp);
             } else {
@@ -252,19 +260,21 @@ __global__ __launch_bounds__(64 * MOE_MAX_K) void expert_down(const uint8_t *__r
     }
     if (c == 0) *reinterpret_cast<float4 *>(&red[slot][4 * q]) = make_float4(r4[0], r4[1], r4[2], r4[3]);
     __syncthreads();
-    if (slot == 0 && lane < 16) {
+    if (slot == 0 && lane < (half ? 8 : 16)) {
         float s = 0.0f;
         for (int j = 0; j < k; ++j) s += red[j][lane];
-        out[(size_t)b * hidden + tile * 16 + lane] += s;
+        out[(size_t)b * hidden + tile * 16 + 8 * hb + lane] += s;
     }
 }
 
 template <int WG, int MW, typename ST>
 static void launch_down_t(marin_gpu *g, const marin_quant_matrix *down, const float *act, const int32_t *ids,
                           const float *weights, size_t tokens, size_t k, size_t hidden, size_t ffn, float *out) {
-    dim3 grid((unsigned)(hidden / 16), (unsigned)tokens);
+    // half tiles while whole tiles leave compute units idle (one token: hidden / 16 workgroups)
+    const int half = MOE_DOWN_HALF && (hidden / 16) * tokens < (size_t)std::max(g->cu_count, 1) ? 1 : 0;
+    dim3 grid((unsigned)((hidden / 16) << half), (unsigned)tokens);
     expert_down<WG, MW, ST><<<grid, dim3(64 * MOE_MAX_K), 0, g->stream>>>(
-        down->codes, (const ST *)down->scales, act, ids, weights, (int)k, (int)hidden, (int)ffn, out);
+        down->codes, (const ST *)down->scales, act, ids, weights, (int)k, (int)hidden, (int)ffn, out, half);
 }
 
 template <typename ST>
