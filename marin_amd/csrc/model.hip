@@ -37,6 +37,30 @@ constexpr size_t CHUNK = MARIN_PREFILL_CHUNK;  // tokens per prompt pass through
 // One decode step's bookkeeping, after the output head left the greedy choice in *best as (total-order key, ~id)
 // (sampler/src/lib.rs:40-48: largest logit, lowest id on ties): record the token, clear the choice for the next
 // head, advance the state (pos += 1, ctx = pos + 1, step += 1) and embed the token's table row into hidden.
+// One int8 embedding row (code x scale, the windowed layout) written by a block: every thread issues all the loads of
+// a pass before its first store, so the pass costs one memory round trip instead of one per element.
+__device__ __forceinline__ void embed_row(const uint8_t *__restrict__ codes, const float *__restrict__ scales,
+                                          size_t row, int cols, int group, float *__restrict__ dst) {
+    constexpr int U = 8;
+    const int groups = cols / group;
+    const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
+    for (int base = 0; base < cols; base += U * (int)blockDim.x) {
+        int cv[U];
+        float sv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = min(base + (int)threadIdx.x + u * (int)blockDim.x, cols - 1);
+            cv[u] = (int8_t)codes[code_offset(row, i, cols, true, 16)];
+            sv[u] = srow[(i / group) * 16];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = base + (int)threadIdx.x + u * (int)blockDim.x;
+            if (i < cols) dst[i] = (float)cv[u] * sv[u];
+        }
+    }
+}
+
 __global__ __launch_bounds__(512) void advance(unsigned long long *best, uint32_t *ids, uint32_t *tokens_out,
                                                uint32_t *state, const uint8_t *__restrict__ codes,
                                                const float *__restrict__ scales, float *__restrict__ hidden, int cols,
@@ -53,11 +77,7 @@ __global__ __launch_bounds__(512) void advance(unsigned long long *best, uint32_
         id_s = id;
     }
     __syncthreads();
-    const size_t row = id_s;
-    const int groups = cols / group;
-    const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
-    for (int i = threadIdx.x; i < cols; i += blockDim.x)
-        hidden[i] = (float)(int8_t)codes[code_offset(row, i, cols, true, 16)] * srow[(i / group) * 16];
+    embed_row(codes, scales, id_s, cols, group, hidden);
 }
 
 // Sets the device state for a pass of `count` tokens at `pos` (pos, ctx = pos + count) and clears the greedy choice
@@ -98,12 +118,7 @@ __global__ __launch_bounds__(512) void advance_batch(unsigned long long *best, u
         id_s = id;
     }
     __syncthreads();
-    const size_t row = id_s;
-    const int groups = cols / group;
-    const float *srow = scales + (row / 16) * (size_t)groups * 16 + (row % 16);
-    float *h = hidden + (size_t)b * cols;
-    for (int i = threadIdx.x; i < cols; i += blockDim.x)
-        h[i] = (float)(int8_t)codes[code_offset(row, i, cols, true, 16)] * srow[(i / group) * 16];
+    embed_row(codes, scales, id_s, cols, group, hidden + (size_t)b * cols);
 }
 
 }  // namespace marin
