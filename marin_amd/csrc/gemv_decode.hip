@@ -169,10 +169,11 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         const int t = tc >> half, hb = tc & half;
         const int la = half ? (c & 7) + 8 * hb + 16 * q : lane;  // the lane whose 16 bytes this lane loads
         const int qs = half ? (q & 1) + 2 * hb : q;               // the rows 4 qs .. + 3 whose scales it takes
-        const uint8_t *p = codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * la;
+        const unsigned uw = (unsigned)w;  // windows are never negative: unsigned index arithmetic needs no sign fixups
+        const uint8_t *p = codes + (size_t)(unsigned)t * tile_bytes + (size_t)uw * (64 * CB) + CB * la;
         if constexpr (BITS == 8) ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
         else ring[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
-        if (slot % WG == 0) sring[slot / WG] = scales4(scales + ((size_t)t * groups + w / WG) * 16 + 4 * qs);
+        if (slot % WG == 0) sring[slot / WG] = scales4(scales + ((size_t)(unsigned)t * groups + uw / WG) * 16 + 4 * qs);
     };
     auto load_item = [&](int i, int slot) {
         load_at(tile_of((int)blockIdx.x + (i / S) * (int)gridDim.x), min(w0 + i % S, windows - 1), slot);
