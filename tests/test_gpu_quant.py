@@ -131,7 +131,9 @@ def test_one_token_products_at_half_and_whole_tile_shapes(gpu, bits, rows, cols)
     assert_close(gpu.download(out), expected, 1e-4)
 
 
-@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 12288), (12288, 4096), (4096, 151936)])
+# (2048, 1000) and (4096, 6144): half tiles at one token (63 tiles, a partial last one; the 8B qkv)
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 12288), (12288, 4096), (4096, 151936), (2048, 1000),
+                                 (4096, 6144)])
 @pytest.mark.parametrize("m_tokens", [1, 4, 8])
 def test_decode_shapes_bf16_layout_within_the_north_star_tolerance(gpu, k, n, m_tokens):
     """Config 1: bf16 activations N(0,1)-like, int8 g128, bf16 scales, bf16 out; max relative error 1e-2 (relative to
