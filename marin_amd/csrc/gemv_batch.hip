@@ -36,8 +36,17 @@ constexpr int BW = 8;      // waves per block
 #ifndef BATCH_RING2
 #define BATCH_RING2 4
 #endif
-template <int TT>
-constexpr int bring() { return TT == 1 ? 8 : BATCH_RING2; }
+#ifndef BATCH_BRES
+#define BATCH_BRES 1
+#endif
+// 8-window slices keep the wave's B fragments (all its windows, every token tile) in registers for the whole launch,
+// so only the codes stream; the registers leave one block per compute unit, and the ring is one slice deep
+template <int SM>
+constexpr bool bres() { return BATCH_BRES && SM == 8; }
+template <int TT, int SM>
+constexpr int bring() { return bres<SM>() ? SM : (TT == 1 ? 8 : BATCH_RING2); }
+template <int SM>
+constexpr int batch_min_blocks() { return bres<SM>() ? 1 : 2; }
 constexpr int BATCH_BLOCKS_PER_CU = 2;
 constexpr int OBUF_TILES = 40;  // tiles a block holds outputs for (the grid covers the matrix in as many rounds)
 
@@ -54,14 +63,15 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 // BITS: 8 or 4 (nibbles stored as code + 8, unpacked to bytes; 8 x the group's limb sums come off the int32 sums);
 // WG: windows per quantization group; TT: token tiles of 4 (1 or 2); SM: windows per wave per tile; ST: scale type.
 template <int BITS, int WG, int TT, int SM, typename ST>
-__global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
+__global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                       const int8_t *__restrict__ limbs,
                                                       const float *__restrict__ exps, const float *__restrict__ rsv,
                                                       const int32_t *__restrict__ lsum, GemvOut out, int tokens,
                                                       int rows, int cols, int tiles) {
     constexpr int CB = BITS == 8 ? 16 : 8;  // code bytes per lane per window
     constexpr int S = SM;
-    constexpr int BRING = bring<TT>();
+    constexpr int BRING = bring<TT, SM>();
+    constexpr bool BRES = bres<SM>();
     __shared__ __align__(16) float red[2][BW][4 * TT][16];
     // the block's finished rows, written out after the main loop: a global store or load inside the loop would
     // sit in the vector memory counter with the ring and make the waits for it drain the ring
@@ -100,14 +110,27 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
     typedef typename std::conditional<BITS == 8, u32x4, u32x2>::type Raw;
     Raw ra[BRING];
     u32x4 rb[BRING][TT];
+    // BRES: the wave's B fragments, window wl of the slice, token tile j; loaded before the ring, so the waits for
+    // them come first in the counter and never drain it
+    u32x4 bq[BRES ? S : 1][TT];
+    if constexpr (BRES) {
+#pragma unroll
+        for (int wl = 0; wl < S; ++wl) {
+            const int w = min(w0 + wl, windows - 1);
+#pragma unroll
+            for (int j = 0; j < TT; ++j) bq[wl][j] = *reinterpret_cast<const u32x4 *>(brow[j] + (size_t)w * ttiles * 1024);
+        }
+    }
     floatx4 rs_[BRING / WG];
     float re[BRING / WG][TT];
     int ro[BRING / WG][TT];
     auto load_at = [&](int t, int w, int slot) {  // window w (clamped to the row) of tile t into ring slot `slot`
         ra[slot] = __builtin_nontemporal_load(
             reinterpret_cast<const Raw *>(codes + (size_t)t * tile_bytes + (size_t)w * 64 * CB + CB * lane));
+        if constexpr (!BRES) {
 #pragma unroll
-        for (int j = 0; j < TT; ++j) rb[slot][j] = *reinterpret_cast<const u32x4 *>(brow[j] + (size_t)w * ttiles * 1024);
+            for (int j = 0; j < TT; ++j) rb[slot][j] = *reinterpret_cast<const u32x4 *>(brow[j] + (size_t)w * ttiles * 1024);
+        }
         if (slot % WG == WG - 1) {  // the group's factors travel with its last window, read at the group's end
             const ST *sp = scales + ((size_t)t * groups + w / WG) * 16 + 4 * q;
             if constexpr (sizeof(ST) == 4) {
@@ -166,7 +189,10 @@ __global__ __launch_bounds__(64 * BW, 2) void gemv_batch(const uint8_t *__restri
             }
             int4v b[TT];
 #pragma unroll
-            for (int j = 0; j < TT; ++j) b[j] = __builtin_bit_cast(int4v, rb[s][j]);
+            for (int j = 0; j < TT; ++j) {
+                if constexpr (BRES) b[j] = __builtin_bit_cast(int4v, bq[s][j]);  // a round is the whole slice
+                else b[j] = __builtin_bit_cast(int4v, rb[s][j]);
+            }
             // items past the block's last one (the ring's tail) contribute zeros and end no tile; with ALIGNED slices
             // items is a multiple of the ring, so there are none
             const bool valid = ALIGNED || i < items;
