@@ -38,6 +38,9 @@ constexpr int RING = DECODE_RING;  // code windows in flight per wave
 #define DECODE_BPC 2
 #endif
 constexpr int DECODE_BLOCKS_PER_CU = DECODE_BPC;
+#ifndef DECODE_BRES
+#define DECODE_BRES 1
+#endif
 #ifndef DECODE_HALF
 #define DECODE_HALF 1
 #endif
@@ -300,6 +303,13 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         rs = 1.0f / sqrtf(total / (float)cols + in.eps);
     }
 
+    // DECODE_BRES: slices one ring round long keep their B fragments in registers for the launch
+    constexpr bool BRES = DECODE_BRES && S == RING;
+    int4v bq[BRES ? S : 1];
+    if constexpr (BRES) {
+#pragma unroll
+        for (int wl = 0; wl < S; ++wl) bq[wl] = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + (c & 3)) * 64 + 16 * q);
+    }
     floatx4 total = (floatx4){0.f, 0.f, 0.f, 0.f};
     floatx4 gsc = total;
     int4v acc = (int4v){0, 0, 0, 0};
@@ -344,7 +354,9 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             const int wl = ALIGNED ? bw + j : i % S;  // window inside the slice
             const int w = w0 + wl;     // window of the row
             // lanes c >= 4 (B columns 4..15, whose sums are never used) read the limbs of lane c % 4
-            const int4v b = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + (c & 3)) * 64 + 16 * q);
+            int4v b;
+            if constexpr (BRES) b = bq[j];  // a round is the whole slice
+            else b = *reinterpret_cast<const int4v *>(limbs + ((size_t)(wave * S + wl) * 4 + (c & 3)) * 64 + 16 * q);
             int4v a;
             if constexpr (BITS == 8) {
                 a = __builtin_bit_cast(int4v, cur);
