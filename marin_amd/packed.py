@@ -34,6 +34,24 @@ class PackedError(ValueError):
     """LoaderError::Packed (crates/loader/src/packed.rs:30-32)."""
 
 
+def _unique_keys(pairs):
+    """object_pairs_hook refusing a key seen twice in one object, as packed_read.rs:139-164 (`unique`) and serde's
+    duplicate-field check do; json.loads alone would keep the last value silently."""
+    out = {}
+    for key, value in pairs:
+        if key in out:
+            raise PackedError(f"duplicate key: {key}")
+        out[key] = value
+    return out
+
+
+def _loads(data):
+    try:
+        return json.loads(data, object_pairs_hook=_unique_keys)
+    except json.JSONDecodeError as e:
+        raise PackedError(str(e)) from None
+
+
 def _regular(path: str) -> bool:
     try:
         return stat.S_ISREG(os.lstat(path).st_mode)
@@ -71,10 +89,7 @@ def read_manifest(directory: str) -> dict:
     if os.path.getsize(path) > 4 << 20:
         raise PackedError("manifest exceeds 4 MiB")
     with open(path, "rb") as f:
-        try:
-            raw = json.loads(f.read())
-        except json.JSONDecodeError as e:
-            raise PackedError(str(e)) from None
+        raw = _loads(f.read())
     keys = {"format", "quantizer", "architecture", "group", "files", "tensors", "source_tensors"}
     if not isinstance(raw, dict) or set(raw) != keys:
         raise PackedError("manifest fields differ from the format's")
@@ -119,10 +134,7 @@ class PackedWeights:
             n = int.from_bytes(f.read(8), "little")
             if n > size - 8:
                 raise PackedError("safetensors header exceeds the file")
-            try:
-                header = json.loads(f.read(n))
-            except json.JSONDecodeError as e:
-                raise PackedError(str(e)) from None
+            header = _loads(f.read(n))
         header.pop("__metadata__", None)
         self._data = np.memmap(path, dtype=np.uint8, mode="r", offset=8 + n)
         spans = []

@@ -451,8 +451,12 @@ uint16_t or_synth_bf16(uint64_t seed, uint64_t stream, uint64_t index, double st
 }
 
 void or_synth_fill(uint64_t seed, uint64_t stream, double std_dev, uint16_t *out, size_t count) {
+    or_synth_fill_at(seed, stream, std_dev, 0, out, count);
+}
+
+void or_synth_fill_at(uint64_t seed, uint64_t stream, double std_dev, uint64_t start, uint16_t *out, size_t count) {
 #pragma omp parallel for schedule(static) num_threads(g_threads)
-    for (long i = 0; i < (long)count; ++i) out[i] = or_synth_bf16(seed, stream, (uint64_t)i, std_dev);
+    for (long i = 0; i < (long)count; ++i) out[i] = or_synth_bf16(seed, stream, start + (uint64_t)i, std_dev);
 }
 
 /* ---- Qwen3 forward: model/src/qwen3/model.rs:81-131, layer.rs:39-105, mlp.rs:22-37 ---- */

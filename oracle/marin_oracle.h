@@ -89,6 +89,8 @@ uint32_t or_argmax(const float *values, size_t n);
  * (which loads checkpoints); pinned by moments and by equality with the device generator. */
 uint16_t or_synth_bf16(uint64_t seed, uint64_t stream, uint64_t index, double std_dev);
 void or_synth_fill(uint64_t seed, uint64_t stream, double std_dev, uint16_t *out, size_t count);
+/* Values start .. start + count - 1 of the same stream (a row range of a synthetic matrix). */
+void or_synth_fill_at(uint64_t seed, uint64_t stream, double std_dev, uint64_t start, uint16_t *out, size_t count);
 
 /* ---- Qwen3 forward (model/src/qwen3/model.rs:81-131, layer.rs:39-105, mlp.rs) over a contiguous f32 KV cache
  * (crates/kv). Weights are int8-quantized (Q8 path) or dense f32 (f64-dot path). ---- */

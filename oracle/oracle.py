@@ -47,6 +47,7 @@ def _load():
         "or_argmax": (C.c_uint32, [P, sz]),
         "or_synth_bf16": (C.c_uint16, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_double]),
         "or_synth_fill": (None, [C.c_uint64, C.c_uint64, C.c_double, P, sz]),
+        "or_synth_fill_at": (None, [C.c_uint64, C.c_uint64, C.c_double, C.c_uint64, P, sz]),
         "or_qwen3_forward": (C.c_int, [P, P, sz, P]),
     }
     for name, (res, args) in sig.items():
@@ -138,9 +139,10 @@ def values(count: int, seed: int) -> np.ndarray:
     return out
 
 
-def synth(seed: int, stream: int, count: int, std: float = 0.02) -> np.ndarray:
+def synth(seed: int, stream: int, count: int, std: float = 0.02, start: int = 0) -> np.ndarray:
+    """Values start .. start + count - 1 of a synthetic stream (bf16 bits)."""
     out = np.zeros(count, np.uint16)
-    lib.or_synth_fill(seed, stream, std, _p(out), count)
+    lib.or_synth_fill_at(seed, stream, std, start, _p(out), count)
     return out
 
 

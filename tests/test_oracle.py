@@ -258,3 +258,65 @@ def test_int8_group32_logits_stay_near_the_dense_logits():
         q2 = o.Qwen3Oracle(cfg, w, 128, group=32).forward(case["prompt_ids"])
         assert np.array_equal(q1, q2)
         assert np.max(np.abs(q1 - dense)) <= 0.10 * np.max(np.abs(dense))
+
+
+# ---- f16 KV rounding: cuda/tests/kv_round/mod.rs:3-18 ----
+def kv_round_f16(x: np.ndarray) -> np.ndarray:
+    """The closed form of cuda/tests/kv_round/mod.rs:5-18 in f32 arithmetic: saturate at 65504, subnormals in steps of
+    2^-24, normals in steps of 2^(biased exponent - 137), ties to even, the sign copied back."""
+    x = np.asarray(x, np.float32)
+    mag = np.abs(x)
+    out = np.empty_like(mag)
+    sat = mag >= np.float32(65504.0)
+    sub = mag < np.float32(6.1035156e-5)
+    nrm = ~sat & ~sub
+    out[sat] = np.float32(65504.0)
+    step = np.float32(2.0 ** -24)
+    out[sub] = np.round(mag[sub] / step).astype(np.float32) * step  # np.round: ties to even
+    e = (mag[nrm].view(np.uint32) >> np.uint32(23)).astype(np.int32)
+    st = np.ldexp(np.float32(1.0), e - 137).astype(np.float32)
+    out[nrm] = np.round(mag[nrm] / st).astype(np.float32) * st
+    return np.copysign(out, x)
+
+
+def oracle_f16_round(x: np.ndarray) -> np.ndarray:
+    return np.array([o.lib.or_f16_to_f32(o.lib.or_f32_to_f16_sat(float(v))) for v in np.asarray(x, np.float32)],
+                    np.float32)
+
+
+def test_f16_store_rounding_matches_the_closed_form_on_every_half_value_and_midpoint():
+    # every finite f16 value round-trips; every midpoint between neighbours rounds to the even one
+    h = np.arange(0, 0x7c00, dtype=np.uint16)
+    exact = np.concatenate([h, h | 0x8000]).view(np.float16).astype(np.float32)
+    assert np.array_equal(oracle_f16_round(exact).view(np.uint32), exact.view(np.uint32))
+    mags = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((mags[:-1] + mags[1:]) / 2).astype(np.float32)  # exact in f32
+    for probe in (mids, -mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))):
+        probe = probe.astype(np.float32)
+        got, want = oracle_f16_round(probe), kv_round_f16(probe)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # numpy's own float16 conversion (round to nearest even) agrees below the saturation point
+    assert np.array_equal(oracle_f16_round(mids), mids.astype(np.float16).astype(np.float32))
+
+
+def test_f16_store_rounding_saturates_keeps_signed_zero_and_quiets_nan():
+    big = np.array([65504.0, 65519.0, 65520.0, 65536.0, 1e6, 3.4e38, np.inf], np.float32)
+    assert np.all(oracle_f16_round(big) == 65504.0)
+    assert np.all(oracle_f16_round(-big) == -65504.0)
+    assert np.array_equal(oracle_f16_round(kv_round_f16(big)), kv_round_f16(big))
+    z = oracle_f16_round(np.array([0.0, -0.0], np.float32))
+    assert z.view(np.uint32).tolist() == [0, 0x80000000]
+    assert np.isnan(oracle_f16_round(np.array([np.nan], np.float32))[0])
+    # the subnormal boundary, the smallest subnormal and half of it (a tie to even: 0), 1.5 of it (to 2)
+    edge = np.array([6.1035156e-5, np.nextafter(np.float32(6.1035156e-5), np.float32(0)), 2.0 ** -24, 2.0 ** -25,
+                     1.5 * 2.0 ** -24, 2.5 * 2.0 ** -24, 1e-10], np.float32)
+    assert np.array_equal(oracle_f16_round(edge).view(np.uint32), kv_round_f16(edge).view(np.uint32))
+    assert oracle_f16_round(edge)[3] == 0.0 and oracle_f16_round(edge)[4] == 2.0 ** -23
+
+
+def test_f16_store_rounding_matches_the_closed_form_on_random_f32_bits():
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 2 ** 32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    assert np.array_equal(oracle_f16_round(x).view(np.uint32), kv_round_f16(x).view(np.uint32))

@@ -144,3 +144,38 @@ def test_a_tensor_missing_from_the_manifest_is_refused(bundle):
     json.dump(m, open(os.path.join(dst, "marin-int8.json"), "w"))
     with pytest.raises(PackedError, match="name mismatch"):
         open_packed(dst)
+
+
+def test_a_duplicate_manifest_key_is_refused(bundle):  # packed_read.rs:139-164 (unique)
+    dst, _ = bundle
+    path = os.path.join(dst, "marin-int8.json")
+    m = json.load(open(path))
+    name, digest = next(iter(m["tensors"].items()))
+    other = [(b + 1) % 256 for b in digest]
+    # the duplicate comes last, so a reader keeping the last value would see a digest that differs from the first
+    text = json.dumps(m)
+    tensors = json.dumps(m["tensors"])
+    dup = tensors[:-1] + ", " + json.dumps(name) + ": " + json.dumps(other) + "}"
+    open(path, "w").write(text.replace(tensors, dup))
+    with pytest.raises(PackedError, match="duplicate key"):
+        open_packed(dst)
+    # a duplicated top-level field too (serde's duplicate field)
+    open(path, "w").write(text[:-1] + ', "group": ' + json.dumps(m["group"]) + "}")
+    with pytest.raises(PackedError, match="duplicate key"):
+        open_packed(dst)
+
+
+def test_a_duplicate_safetensors_header_key_is_refused(bundle):  # safetensors.rs:82-87 (packed_read::parse)
+    dst, _ = bundle
+    path = os.path.join(dst, "model.safetensors")
+    raw = open(path, "rb").read()
+    n = int.from_bytes(raw[:8], "little")
+    header = json.loads(raw[8:8 + n])
+    name = next(k for k in header if k != "__metadata__")
+    text = json.dumps(header)
+    text = text[:-1] + ", " + json.dumps(name) + ": " + json.dumps(header[name]) + "}"
+    body = text.encode()
+    body += b" " * ((8 - len(body) % 8) % 8)
+    open(path, "wb").write(len(body).to_bytes(8, "little") + body + raw[8 + n:])
+    with pytest.raises(PackedError, match="duplicate key"):
+        open_packed(dst)
