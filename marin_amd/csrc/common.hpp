@@ -133,6 +133,13 @@ struct marin_gpu {
     void *work = nullptr;
     size_t work_bytes = 0;
     void *workspace(size_t bytes);
+    // Device fault word: kernels that meet input the reference rejects (non-finite router logits) set a bit and
+    // carry on with harmless values; the next blocking call (synchronize, download) reports it and clears it.
+    uint32_t *fault = nullptr;
+    void check_fault();
+    // Gpu::set_fast_attention (crates/cuda/src/attention.rs:81-86): prompt passes over an f16 cache use the
+    // matrix-core attention when set (the default; MARIN_NO_FA=1 in the environment clears it at creation).
+    bool fast_attention = true;
 
     // Launch accounting. With a profile attached, every launch is tagged with its kind, algorithmic bytes and kernel
     // name. The product and attention launchers then launch through hipExtLaunchKernelGGL with the two events of
@@ -159,3 +166,8 @@ struct marin_gpu {
     void kernel_events(hipEvent_t &start, hipEvent_t &stop);
     void launched(int kind = OTHER, double bytes = 0.0, const char *name = nullptr);
 };
+
+namespace marin {
+// Bits of marin_gpu::fault.
+constexpr uint32_t FAULT_ROUTER_NONFINITE = 1u;
+}  // namespace marin

@@ -104,6 +104,7 @@ void *marin_gpu::workspace(size_t bytes) {
 void marin_gpu::destroy() {
     (void)hipStreamSynchronize(stream);
     if (work) (void)hipFree(work);
+    if (fault) (void)hipFree(fault);
     if (pinned) (void)hipHostFree(pinned);
     for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(stream);
@@ -125,6 +126,20 @@ void marin_gpu::download(void *dst, const void *src, size_t bytes) {
     HIP_CHECK(hipStreamSynchronize(stream));
     traffic.downloads++;
     traffic.download_bytes += bytes;
+    check_fault();
+}
+
+void marin_gpu::check_fault() {
+    if (!fault) return;
+    uint32_t word = 0;
+    HIP_CHECK(hipMemcpy(&word, fault, 4, hipMemcpyDeviceToHost));
+    if (!word) return;
+    HIP_CHECK(hipMemset(fault, 0, 4));
+    if (word & FAULT_ROUTER_NONFINITE)
+        // ModelError::InvalidConfig("nonfinite ... router logits"), model/src/granite/layer.rs:42-47
+        throw Error(MARIN_SELF_CHECK, "nonfinite router logits (their tokens were routed to experts 0..k-1 with "
+                                      "weight 0)");
+    throw Error(MARIN_SELF_CHECK, "device fault word " + std::to_string(word));
 }
 
 hipEvent_t marin_gpu::next_event() {
@@ -200,11 +215,29 @@ marin_status marin_gpu_new(marin_gpu **out) {
         g->device = 0;
         g->cu_count = prop.multiProcessorCount;
         g->name = prop.name;
+        if (g->name.empty()) {
+            char nm[256] = {0};
+            if (hipDeviceGetName(nm, sizeof(nm) - 1, 0) == hipSuccess) g->name = nm;
+        }
+        if (g->name.empty())
+            g->name = "AMD " + arch.substr(0, arch.find(':')) + " (" + std::to_string(prop.multiProcessorCount) + " CUs)";
         g->arch = arch;
+        {
+            const char *nofa = getenv("MARIN_NO_FA");
+            g->fast_attention = !(nofa && *nofa && *nofa != '0');
+        }
         hipError_t e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
             delete g;
             hip_check(e, "hipStreamCreate");
+        }
+        e = hipMalloc((void **)&g->fault, 256);
+        if (e == hipSuccess) e = hipMemset(g->fault, 0, 256);
+        if (e != hipSuccess) {
+            (void)hipStreamDestroy(g->stream);
+            if (g->fault) (void)hipFree(g->fault);
+            delete g;
+            hip_check(e, "hipMalloc (fault word)");
         }
         *out = g;
     });
@@ -229,10 +262,19 @@ marin_status marin_gpu_info_get(marin_gpu *g, marin_gpu_info *out) {
 }
 
 marin_status marin_gpu_synchronize(marin_gpu *g) {
-    return guard([&] { HIP_CHECK(hipStreamSynchronize(g->stream)); });
+    return guard([&] {
+        HIP_CHECK(hipStreamSynchronize(g->stream));
+        g->check_fault();
+    });
 }
 
 void *marin_gpu_stream(marin_gpu *g) { return (void *)g->stream; }
+
+marin_status marin_gpu_bind_to_thread(marin_gpu *g) {
+    return guard([&] { HIP_CHECK(hipSetDevice(g->device)); });
+}
+
+void marin_set_fast_attention(marin_gpu *g, int on) { g->fast_attention = on != 0; }
 
 marin_status marin_gpu_traffic(marin_gpu *g, marin_traffic *out) {
     return guard([&] { *out = g->traffic; });

@@ -30,6 +30,7 @@ struct GemvIn {
     // output row r of the product is logical row r of that concatenation.
     const int32_t *tile_map = nullptr;
     int map_tiles = 0, map_count = 0;
+    int map_blocks = 0;  // blocks of map_tiles tiles in the matrix: map entries are clamped below it
 };
 
 struct GemvOut {

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     // a wave-uniform lane read: a per-item load of the map would sit behind the code windows already in flight and
     // wait for all of them.
     const int *map_p = in.tile_map ? in.tile_map : reinterpret_cast<const int *>(in.x);
-    const int map_v = map_p[min(lane, max(in.map_count, 1) - 1)];
+    const int map_v = min(max(map_p[min(lane, max(in.map_count, 1) - 1)], 0), max(in.map_blocks, 1) - 1);
 
     // ---- the activations, block-wide: in round r, thread T holds the 16 consecutive columns RC r + 16 T .. + 16
     // (RC = 1024 DW columns per round), i.e. quarter T % 4 of window 16 DW r + T / 4: exactly what the B operand of
@@ -466,6 +466,8 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     if (in.tile_map && (in.map_count < 1 || in.map_count > MAP_MAX || in.map_tiles < 1))
         unsupported("tile map entries (1 to 64)", MAP_MAX, (size_t)in.map_count);
     const int tiles = in.tile_map ? in.map_tiles * in.map_count : (int)(w->rows_padded / 16);
+    if (in.tile_map && (in.map_blocks < 1 || (size_t)in.map_blocks * in.map_tiles * 16 > w->rows_padded))
+        shape("tile map blocks (within the matrix)", w->rows_padded / 16 / in.map_tiles, (size_t)in.map_blocks);
     const int rows = in.tile_map ? tiles * 16 : (int)w->rows;
     const size_t gpad = (size_t)((groups + 3) & ~3);
     const size_t lds = (size_t)DW * SM * 256 + gpad * 4 + (BITS == 4 ? gpad * 16 : 0) + (size_t)(2 * DW * 16 + DW) * 4;

@@ -44,7 +44,7 @@ __device__ __forceinline__ unsigned total_key(float v) {
 // ties) in descending order; weights p_e, or p_e / sum of the k when `renorm`.
 __global__ __launch_bounds__(ROUTE_THREADS) void moe_route(const float *__restrict__ logits, int experts, int k,
                                                            int renorm, int32_t *__restrict__ ids,
-                                                           float *__restrict__ weights) {
+                                                           float *__restrict__ weights, uint32_t *__restrict__ fault) {
     __shared__ float p_s[1024];
     __shared__ unsigned long long best_s[ROUTE_THREADS / 64];
     __shared__ float red_s[ROUTE_THREADS / 64];
@@ -53,10 +53,25 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route(const float *__restri
     const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *l = logits + (size_t)b * experts;
     float mx = -INFINITY;
-    for (int e = threadIdx.x; e < experts; e += ROUTE_THREADS) mx = fmaxf(mx, l[e]);
+    bool finite = true;
+    for (int e = threadIdx.x; e < experts; e += ROUTE_THREADS) {
+        const float v = l[e];
+        finite = finite && fabsf(v) <= 3.402823466e38f;  // false for NaN and both infinities
+        mx = fmaxf(mx, v);
+    }
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if (lane == 0) red_s[wave] = mx;
-    __syncthreads();
+    // The reference refuses non-finite router logits (model/src/granite/layer.rs:42-47). Such a token is routed to
+    // experts 0..k-1 with weight 0, so nothing downstream reads outside the experts, and the fault word reports it
+    // at the next blocking call.
+    if (__syncthreads_or(!finite)) {
+        if (threadIdx.x < k) {
+            ids[(size_t)b * k + threadIdx.x] = (int32_t)threadIdx.x;
+            weights[(size_t)b * k + threadIdx.x] = 0.0f;
+        }
+        if (threadIdx.x == 0) *fault = FAULT_ROUTER_NONFINITE;
+        return;
+    }
     mx = red_s[0];
     for (int w = 1; w < ROUTE_THREADS / 64; ++w) mx = fmaxf(mx, red_s[w]);
     __syncthreads();
@@ -112,11 +127,11 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route(const float *__restri
 
 // The routing plan of a decode batch (tokens * k <= 64 selections), one wave: the distinct selected experts in
 // ascending order and, per (distinct expert, token), the slot that selected it or -1 (layout in gemm.hpp).
-__global__ __launch_bounds__(64) void moe_plan(const int32_t *__restrict__ ids, int tokens, int k,
+__global__ __launch_bounds__(64) void moe_plan(const int32_t *__restrict__ ids, int tokens, int k, int experts,
                                                int32_t *__restrict__ plan) {
     __shared__ int32_t slots[MOE_PLAN_MAX * MOE_BATCH];
     const int lane = threadIdx.x, n = tokens * k;
-    const int id = ids[min(lane, n - 1)];
+    const int id = min(max(ids[min(lane, n - 1)], 0), experts - 1);  // ids from outside stay inside the experts
     bool first = lane < n;  // first occurrence of its expert
     int rank = 0;           // distinct experts below it
     for (int j = 0; j < n; ++j) {
@@ -148,8 +163,8 @@ __global__ __launch_bounds__(64 * MOE_MAX_K) void expert_down(const uint8_t *__r
                                                               const ST *__restrict__ scales,
                                                               const float *__restrict__ act,
                                                               const int32_t *__restrict__ ids,
-                                                              const float *__restrict__ weights, int k, int hidden,
-                                                              int ffn, float *__restrict__ out, int half) {
+                                                              const float *__restrict__ weights, int k, int experts,
+                                                              int hidden, int ffn, float *__restrict__ out, int half) {
     __shared__ __align__(16) int8_t limbs[MOE_MAX_K][MW][4][64];
     __shared__ float gdown[MOE_MAX_K][MW];
     __shared__ float red[MOE_MAX_K][16];
@@ -164,7 +179,7 @@ __global__ __launch_bounds__(64 * MOE_MAX_K) void expert_down(const uint8_t *__r
     const int windows = ffn >> 6, groups = windows / WG;
     const int tiles_per_expert = hidden / 16;
     const bool on = slot < k;
-    const int e = ids[(size_t)b * k + min(slot, k - 1)];
+    const int e = min(max(ids[(size_t)b * k + min(slot, k - 1)], 0), experts - 1);
     const size_t ptile = (size_t)e * tiles_per_expert + tile;
     // the expert's activation row first (lane L takes 16 consecutive columns), then every code window of the tile
     const float *arow = act + ((size_t)b * k + min(slot, k - 1)) * ffn;
@@ -274,7 +289,8 @@ static void launch_down_t(marin_gpu *g, const marin_quant_matrix *down, const fl
     const int half = MOE_DOWN_HALF && (hidden / 16) * tokens < (size_t)std::max(g->cu_count, 1) ? 1 : 0;
     dim3 grid((unsigned)((hidden / 16) << half), (unsigned)tokens);
     expert_down<WG, MW, ST><<<grid, dim3(64 * MOE_MAX_K), 0, g->stream>>>(
-        down->codes, (const ST *)down->scales, act, ids, weights, (int)k, (int)hidden, (int)ffn, out, half);
+        down->codes, (const ST *)down->scales, act, ids, weights, (int)k, (int)(down->rows / hidden), (int)hidden,
+        (int)ffn, out, half);
 }
 
 template <typename ST>
@@ -330,7 +346,7 @@ static void launch_moe(marin_gpu *g, const MoeArgs &a, int part = 0) {
         // a decode batch: every distinct selected expert's gate_up rows read once for all tokens
         uint8_t *ws = (uint8_t *)g->workspace(moe_scratch_bytes(a));
         int32_t *plan = (int32_t *)(ws + moe_scratch_bytes(a) - MOE_PLAN_WORDS * 4);
-        moe_plan<<<1, 64, 0, g->stream>>>(a.ids, (int)a.tokens, (int)a.k, plan);
+        moe_plan<<<1, 64, 0, g->stream>>>(a.ids, (int)a.tokens, (int)a.k, (int)a.experts, plan);
         g->launched();
         GemvIn in;
         in.mode = a.norm ? IN_NORM : IN_F32;
@@ -353,6 +369,7 @@ static void launch_moe(marin_gpu *g, const MoeArgs &a, int part = 0) {
         in.tile_map = a.ids + t * a.k;
         in.map_tiles = (int)(2 * a.ffn / 16);
         in.map_count = (int)a.k;
+        in.map_blocks = (int)a.experts;
         GemvOut o;
         o.mode = OUT_SILU;
         o.y = a.act + t * a.k * a.ffn;
@@ -393,7 +410,8 @@ marin_status marin_moe_route(marin_gpu *g, const marin_buffer *logits, size_t to
         if (!ids || ids->dtype != MARIN_U32 || ids->len < tokens * k) shape("expert ids (u32)", tokens * k, ids ? ids->len : 0);
         f32_of(weights, tokens * k, "expert weights");
         moe_route<<<(unsigned)tokens, ROUTE_THREADS, 0, g->stream>>>((const float *)logits->data, (int)experts, (int)k,
-                                                                     renorm, (int32_t *)ids->data, (float *)weights->data);
+                                                                     renorm, (int32_t *)ids->data, (float *)weights->data,
+                                                                     g->fault);
         g->launched();
     });
 }

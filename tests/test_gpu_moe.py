@@ -6,6 +6,8 @@ on hand cases (ties go to the lowest expert id, like the sampler's argmax, sampl
 weights sum to 1) and against an f64 softmax/top-k; the expert FFN against the f64 product of the dequantized experts
 (the oracle's quantizer) with the GPU's own routing, tolerance 2e-4 (1 + |e|).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -129,3 +131,85 @@ def test_expert_ffn_rejects_shapes_it_cannot_run(gpu):
         gpu.moe_ffn(gate_up, down, x, None, 1e-6, ids, w, 1, experts, 9, gpu.zeros(9 * ffn), gpu.zeros(hidden))
     with pytest.raises(m.Shape):
         gpu.moe_ffn(gate_up, down, x, None, 1e-6, ids, w, 1, experts + 1, 2, gpu.zeros(2 * ffn), gpu.zeros(hidden))
+
+
+def test_nonfinite_router_logits_are_reported_and_route_nowhere_harmful(gpu):
+    """model/src/granite/layer.rs:42-47 refuses non-finite router logits. The routing kernel gives such a token
+    experts 0..k-1 with weight 0 (nothing downstream reads outside the experts) and the next blocking call reports
+    SelfCheck; finite tokens of the same launch route normally, and the report is cleared once made."""
+    experts, k = 16, 4
+    logits = np.random.default_rng(3).standard_normal((4, experts)).astype(np.float32)
+    logits[1, 5] = np.nan
+    logits[2, 0] = np.inf
+    logits[3, 9] = -np.inf
+    ids = gpu.typed(m.Dtype.U32, 4 * k)
+    w = gpu.zeros(4 * k)
+    gpu.moe_route(gpu.upload(logits.ravel()), 4, experts, k, True, ids, w)
+    with pytest.raises(m.SelfCheck, match="nonfinite router logits"):
+        gpu.synchronize()
+    got_ids = gpu.download_typed(ids).reshape(4, k).astype(np.int64)
+    got_w = gpu.download(w).reshape(4, k)
+    for t in (1, 2, 3):
+        assert got_ids[t].tolist() == list(range(k)) and np.all(got_w[t] == 0.0)
+    ref_ids, ref_w = route_reference(logits[:1], k, True)
+    assert got_ids[0].tolist() == ref_ids[0].tolist()
+    assert np.abs(got_w[0] - ref_w[0]).max() <= 1e-6
+    # the expert FFN over those routes reads only real experts and adds nothing for the weight-0 tokens
+    hidden, ffn = 256, 128
+    gate_up = gpu.quantized_synthetic(experts * 2 * ffn, hidden, 128, 1, 1)
+    down = gpu.quantized_synthetic(experts * hidden, ffn, 128, 1, 2)
+    x = gpu.upload(np.ones(4 * hidden, np.float32))
+    out = gpu.zeros(4 * hidden)
+    gpu.moe_ffn(gate_up, down, x, None, 1e-6, ids, w, 4, experts, k, gpu.zeros(4 * k * ffn), out)
+    res = gpu.download(out).reshape(4, hidden)
+    assert np.all(res[1:] == 0.0) and np.any(res[0] != 0.0)
+    gpu.synchronize()  # reported once, then clear
+
+
+def synth_expert_rows(seed, stream, row0, rows, cols, group=128):
+    """Rows row0 .. row0 + rows - 1 of a device-synthetic int8 matrix (marin_quantized_synthetic), quantized by the
+    oracle: quantization is per row, so a row range quantizes exactly as inside the whole matrix. f64 dequantized."""
+    w = o.synth(seed, stream, rows * cols, start=row0 * cols)
+    c, s = o.quantize(w, rows, cols, 8, group)
+    return (c.view(np.int8).reshape(rows, cols // group, group).astype(np.float64)
+            * s.reshape(rows, cols // group, 1).astype(np.float64)).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_expert_ffn_at_the_qwen3_30b_a3b_shape(gpu, tokens):
+    """Config 4 at its own size: 128 experts of FFN 768 over hidden 2048, int8 g128, top-8 with renormalized softmax
+    weights, batch 1 (one-token product with the expert tile map) and 8 (grouped batch); the selected experts
+    dequantized by the oracle from the same synthetic streams, f64 product, 2e-4 (1 + |e|)."""
+    experts, k, hidden, ffn, seed = 128, 8, 2048, 768, 29
+    print(f"case config-4 tokens={tokens}", flush=True)
+    o.set_threads(min(16, os.cpu_count() or 1))
+    gate_up = gpu.quantized_synthetic(experts * 2 * ffn, hidden, 128, seed, 1)
+    down = gpu.quantized_synthetic(experts * hidden, ffn, 128, seed, 2)
+    rng = np.random.default_rng(40 + tokens)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    norm = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    out0 = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    ids_b = gpu.typed(m.Dtype.U32, tokens * k)
+    w_b = gpu.zeros(tokens * k)
+    gpu.moe_route(gpu.upload(logits.ravel()), tokens, experts, k, True, ids_b, w_b)
+    ids = gpu.download_typed(ids_b).reshape(tokens, k).astype(np.int64)
+    wts = gpu.download(w_b).reshape(tokens, k).astype(np.float64)
+    ref_ids, ref_w = route_reference(logits, k, True)
+    assert (ids == ref_ids).all() and np.abs(wts - ref_w).max() <= 1e-6
+    act = gpu.zeros(tokens * k * ffn)
+    out = gpu.upload(out0.ravel())
+    gpu.moe_ffn(gate_up, down, gpu.upload(x.ravel()), gpu.upload(norm), 1e-6, ids_b, w_b, tokens, experts, k, act,
+                out)
+    got = gpu.download(out).reshape(tokens, hidden)
+    xs = x.astype(np.float64)
+    xn = xs / np.sqrt((xs * xs).mean(-1, keepdims=True) + 1e-6) * norm.astype(np.float64)
+    exp = out0.astype(np.float64).copy()
+    for e in sorted(set(ids.ravel().tolist())):
+        gu = synth_expert_rows(seed, 1, e * 2 * ffn, 2 * ffn, hidden)
+        dn = synth_expert_rows(seed, 2, e * hidden, hidden, ffn)
+        for t, j in zip(*np.nonzero(ids == e)):
+            a = gu[0::2] @ xn[t]
+            a = a / (1.0 + np.exp(-a)) * (gu[1::2] @ xn[t])
+            exp[t] += wts[t, j] * (dn @ a)
+    assert_close(got.ravel(), exp.ravel(), 2e-4)
