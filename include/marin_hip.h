@@ -59,6 +59,11 @@ marin_status marin_gpu_info_get(marin_gpu *gpu, marin_gpu_info *out); /* Gpu::in
 marin_status marin_gpu_synchronize(marin_gpu *gpu);                   /* Gpu::synchronize, gpu.rs:244 */
 /* The context's stream (hipStream_t), for interop only. */
 void *marin_gpu_stream(marin_gpu *gpu);
+/* Gpu::bind_to_thread (gpu.rs:238-242): makes the context's device current on the calling thread. */
+marin_status marin_gpu_bind_to_thread(marin_gpu *gpu);
+/* Gpu::set_fast_attention (attention.rs:81-86): whether prompt passes over an f16 cache with head size 64 or 128 use
+ * the matrix-core attention (the default); off, they take the vector-ALU kernel, as other caches always do. */
+void marin_set_fast_attention(marin_gpu *gpu, int on);
 
 /* Traffic counters: crates/cuda/src/counters.rs:10-89 (struct Traffic, Gpu::traffic :102). */
 typedef struct marin_traffic {
@@ -134,6 +139,34 @@ marin_status marin_matmul_quant_precise(marin_gpu *gpu, const marin_quant_matrix
 marin_status marin_matmul_quant_bf16(marin_gpu *gpu, const marin_quant_matrix *w, const marin_buffer *x,
                                      size_t tokens, marin_buffer *out);
 
+/* ---- dense bf16 matrices: crates/cuda/src/gpu.rs:87-93 (DeviceMatrix), gpu.rs:248-268, matmul.rs:16-205 ---- */
+typedef struct marin_matrix marin_matrix; /* DeviceMatrix: bf16 bits, row-major [rows][cols] */
+
+/* Gpu::upload_matrix (gpu.rs:248-268): checks len == rows * cols (Shape) and the product (Overflow). */
+marin_status marin_upload_matrix(marin_gpu *gpu, size_t rows, size_t cols, const uint16_t *bits, size_t len,
+                                 marin_matrix **out);
+void marin_matrix_free(marin_matrix *m);
+void marin_matrix_shape(const marin_matrix *m, size_t *rows, size_t *cols);
+/* Gpu::embed (ops.rs:55-73): out[t] = row ids[t] of a bf16 table as f32. Ids >= rows, more ids than `scratch`
+ * holds, or out.len != n * cols are refused (Shape) before anything is copied. */
+marin_status marin_embed(marin_gpu *gpu, const marin_matrix *table, const uint32_t *ids, size_t n,
+                         marin_tokens *scratch, marin_buffer *out);
+/* Gpu::matmul (matmul.rs:16-24): out[t][r] = dot(w[r], x[t]); f32 activations, f32 accumulation; from 16 tokens with
+ * cols a multiple of 16 on the matrix cores with the activations split into three bf16 parts, so every product is
+ * exact (matmul.rs:51 chooses the kernel the same way). */
+marin_status marin_matmul(marin_gpu *gpu, const marin_matrix *w, const marin_buffer *x, size_t tokens,
+                          marin_buffer *out);
+/* Gpu::matmul_precise (matmul.rs:26-35): the same product on the vector ALUs in f32 at every token count. */
+marin_status marin_matmul_precise(marin_gpu *gpu, const marin_matrix *w, const marin_buffer *x, size_t tokens,
+                                  marin_buffer *out);
+/* Gpu::matmul_pair / matmul_triple (matmul.rs:101-166): matrices sharing x, each with its own output; the same bits
+ * as separate matmuls. Mismatched columns or buffer sizes are refused (Shape) before any launch. */
+marin_status marin_matmul_pair(marin_gpu *gpu, const marin_matrix *w0, const marin_matrix *w1, const marin_buffer *x,
+                               size_t tokens, marin_buffer *y0, marin_buffer *y1);
+marin_status marin_matmul_triple(marin_gpu *gpu, const marin_matrix *w0, const marin_matrix *w1,
+                                 const marin_matrix *w2, const marin_buffer *x, size_t tokens, marin_buffer *y0,
+                                 marin_buffer *y1, marin_buffer *y2);
+
 /* ---- elementwise ops: crates/cuda/src/ops.rs:110-236 ---- */
 marin_status marin_rms_norm(marin_gpu *gpu, marin_buffer *x, const marin_buffer *weight, float eps); /* ops.rs:110 */
 marin_status marin_rms_norm_into(marin_gpu *gpu, const marin_buffer *x, const marin_buffer *weight,
@@ -162,6 +195,10 @@ marin_status marin_kv_advance(marin_kv *kv, size_t tokens);  /* kv.rs:186 */
 marin_status marin_kv_truncate(marin_kv *kv, size_t len);    /* kv.rs:176 */
 void marin_kv_clear(marin_kv *kv);                            /* kv.rs:170 */
 size_t marin_kv_len(const marin_kv *kv);                      /* kv.rs:85 */
+int marin_kv_is_empty(const marin_kv *kv);                    /* kv.rs:89 */
+marin_kv_format marin_kv_format_of(const marin_kv *kv);       /* DeviceKv::format, kv.rs:81 */
+/* DeviceKv::auxiliary_bytes (kv.rs:144-150): the split-attention scratch and the device page table. */
+size_t marin_kv_auxiliary_bytes(const marin_kv *kv);
 size_t marin_kv_capacity(const marin_kv *kv);                 /* kv.rs:93 */
 size_t marin_kv_pages_held(const marin_kv *kv);               /* kv.rs:98 */
 size_t marin_kv_pages_in_use(const marin_kv *kv);             /* kv.rs:111 */

@@ -174,6 +174,31 @@ class DeviceQuantMatrix:
             self._h = None
 
 
+class DeviceMatrix:
+    """gpu.rs:87-93: a bf16 matrix, row-major, on the device."""
+
+    def __init__(self, handle):
+        self._h = handle
+        r, c = C.c_size_t(), C.c_size_t()
+        lib.marin_matrix_shape(handle, C.byref(r), C.byref(c))
+        self._rows, self._cols = r.value, c.value
+
+    @property
+    def handle(self):
+        return self._h
+
+    def rows(self) -> int:
+        return self._rows
+
+    def cols(self) -> int:
+        return self._cols
+
+    def __del__(self):
+        if getattr(self, "_h", None) and alive():
+            lib.marin_matrix_free(self._h)
+            self._h = None
+
+
 class Traffic:
     def __init__(self, t: TrafficC):
         for f, _ in TrafficC._fields_:
@@ -227,6 +252,38 @@ class Gpu:
 
     def synchronize(self) -> None:
         check(lib.marin_gpu_synchronize(self._h))
+
+    def bind_to_thread(self) -> None:
+        check(lib.marin_gpu_bind_to_thread(self._h))
+
+    def set_fast_attention(self, on: bool) -> None:
+        lib.marin_set_fast_attention(self._h, int(bool(on)))
+
+    # ---- dense bf16 matrices (gpu.rs:248, matmul.rs, ops.rs:55) ----
+    def upload_matrix(self, rows: int, cols: int, bits) -> "DeviceMatrix":
+        a = np.ascontiguousarray(np.asarray(bits, dtype=np.uint16)).ravel()
+        h = _out()
+        check(lib.marin_upload_matrix(self._h, rows, cols, a.ctypes.data, a.size, C.byref(h)))
+        return DeviceMatrix(h)
+
+    def embed(self, table: "DeviceMatrix", ids, scratch: "Tokens", out: "Buffer") -> None:
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32)).ravel()
+        check(lib.marin_embed(self._h, table.handle, a.ctypes.data, a.size, scratch._h, out.handle))
+
+    def matmul(self, w: "DeviceMatrix", x: "Buffer", tokens: int, out: "Buffer") -> None:
+        check(lib.marin_matmul(self._h, w.handle, x.handle, tokens, out.handle))
+
+    def matmul_precise(self, w: "DeviceMatrix", x: "Buffer", tokens: int, out: "Buffer") -> None:
+        check(lib.marin_matmul_precise(self._h, w.handle, x.handle, tokens, out.handle))
+
+    def matmul_pair(self, ws, x: "Buffer", tokens: int, ys) -> None:
+        (w0, w1), (y0, y1) = ws, ys
+        check(lib.marin_matmul_pair(self._h, w0.handle, w1.handle, x.handle, tokens, y0.handle, y1.handle))
+
+    def matmul_triple(self, ws, x: "Buffer", tokens: int, ys) -> None:
+        (w0, w1, w2), (y0, y1, y2) = ws, ys
+        check(lib.marin_matmul_triple(self._h, w0.handle, w1.handle, w2.handle, x.handle, tokens, y0.handle,
+                                      y1.handle, y2.handle))
 
     def traffic(self) -> Traffic:
         t = TrafficC()
@@ -418,6 +475,15 @@ class DeviceKv:
     def len(self) -> int:
         return int(lib.marin_kv_len(self._h))
 
+    def is_empty(self) -> bool:
+        return bool(lib.marin_kv_is_empty(self._h))
+
+    def kv_format(self) -> KvFormat:
+        return KvFormat(int(lib.marin_kv_format_of(self._h)))
+
+    def auxiliary_bytes(self) -> int:
+        return int(lib.marin_kv_auxiliary_bytes(self._h))
+
     def capacity(self) -> int:
         return int(lib.marin_kv_capacity(self._h))
 
@@ -476,6 +542,6 @@ class PagePool:
                                               tables.shape[1], ctx.ctypes.data, ctx.size, heads, out.handle))
 
 
-__all__ = ["Gpu", "Buffer", "Tokens", "DeviceQuantMatrix", "DeviceKv", "KvFormat", "PagePool", "Dtype",
+__all__ = ["Gpu", "Buffer", "Tokens", "DeviceQuantMatrix", "DeviceMatrix", "DeviceKv", "KvFormat", "PagePool", "Dtype",
            "PAGE_TOKENS", "SLAB_PAGES", "pages_for", "HipError", "Unavailable", "Driver", "Shape", "KvMemory",
            "Overflow", "SelfCheck", "Unsupported", "check"]

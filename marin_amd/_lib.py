@@ -51,6 +51,19 @@ SIGNATURES = {
     "marin_gpu_info_get": (st, [P, C.POINTER(GpuInfo)]),
     "marin_gpu_synchronize": (st, [P]),
     "marin_gpu_stream": (P, [P]),
+    "marin_gpu_bind_to_thread": (st, [P]),
+    "marin_set_fast_attention": (None, [P, C.c_int]),
+    "marin_upload_matrix": (st, [P, sz, sz, P, sz, PP]),
+    "marin_matrix_free": (None, [P]),
+    "marin_matrix_shape": (None, [P, C.POINTER(sz), C.POINTER(sz)]),
+    "marin_embed": (st, [P, P, P, sz, P, P]),
+    "marin_matmul": (st, [P, P, P, sz, P]),
+    "marin_matmul_precise": (st, [P, P, P, sz, P]),
+    "marin_matmul_pair": (st, [P, P, P, P, sz, P, P]),
+    "marin_matmul_triple": (st, [P, P, P, P, P, sz, P, P, P]),
+    "marin_kv_is_empty": (C.c_int, [P]),
+    "marin_kv_format_of": (C.c_int, [P]),
+    "marin_kv_auxiliary_bytes": (sz, [P]),
     "marin_gpu_traffic": (st, [P, C.POINTER(TrafficC)]),
     "marin_mark_new": (st, [P, PP]),
     "marin_mark_since": (st, [P, P, C.POINTER(C.c_double)]),
