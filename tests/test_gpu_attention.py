@@ -252,13 +252,20 @@ def test_half_formats_round_on_store_and_attend_in_f32(gpu, fmt):  # kv_formats.
         mir.check_every_kernel(gpu)
 
 
-def test_batched_paged_attention_over_a_shuffled_shared_pool(gpu):
-    """Config 2 shape, scaled down: 32 Q / 8 KV heads, head_dim 128, 16-token pages, ragged contexts, shuffled page
-    tables from one pool; bf16 in and out, against the f64 reference of each sequence (max relative 1e-2)."""
-    rng = np.random.default_rng(5)
-    batch, heads, kvh, hd, pt = 4, 32, 8, 128, 16
-    ctx = rng.integers(1, 700, size=batch).astype(np.uint32)
-    ctx[0] = 1
+@pytest.mark.parametrize("batch,lo,hi", [(4, 1, 700), (16, 512, 8193)])
+def test_batched_paged_attention_over_a_shuffled_shared_pool(gpu, batch, lo, hi):
+    """Config 2: 32 Q / 8 KV heads, head_dim 128, 16-token pages, ragged contexts, shuffled page tables from one pool;
+    bf16 in and out, against the f64 reference of each sequence (max relative 1e-2). At its own size (batch 16,
+    contexts uniform in [512, 8192], the longest pinned to 8192 and the shortest to 512) the longest sequences are
+    split into more chunks than one merge level takes; the small case adds a one-position context."""
+    print(f"case batch={batch} ctx in [{lo}, {hi})", flush=True)
+    rng = np.random.default_rng(5 + batch)
+    heads, kvh, hd, pt = 32, 8, 128, 16
+    ctx = rng.integers(lo, hi, size=batch).astype(np.uint32)
+    if lo == 1:
+        ctx[0] = 1
+    else:
+        ctx[0], ctx[-1] = hi - 1, lo
     pages_each = [-(-int(c) // pt) for c in ctx]
     total = sum(pages_each)
     perm = rng.permutation(total)

@@ -3,6 +3,9 @@
 The oracle is the f64 product of the dequantized rows (quant.rs:19-37) on the same seeded inputs; the shape grid,
 group sizes, token counts, extremes and rejections are the reference's own.
 """
+import functools
+import os
+
 import numpy as np
 import pytest
 
@@ -132,31 +135,51 @@ def test_one_token_products_at_half_and_whole_tile_shapes(gpu, bits, rows, cols)
 
 
 # (2048, 1000) and (4096, 6144): half tiles at one token (63 tiles, a partial last one; the 8B qkv)
+@functools.lru_cache(maxsize=1)
+def config1_matrix(k, n, bits):
+    """The quantized synthetic matrix of one config-1 case (kept for the next token count of the same shape)."""
+    o.set_threads(min(16, os.cpu_count() or 1))
+    wbits = o.synth(11, 100 + n + k, n * k)
+    codes, scales = o.quantize(wbits, n, k, bits, 128)
+    return codes, scales
+
+
+@pytest.mark.parametrize("m_tokens", [1, 4, 8])
 @pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 12288), (12288, 4096), (4096, 151936), (2048, 1000),
                                  (4096, 6144)])
-@pytest.mark.parametrize("m_tokens", [1, 4, 8])
-def test_decode_shapes_bf16_layout_within_the_north_star_tolerance(gpu, k, n, m_tokens):
-    """Config 1: bf16 activations N(0,1)-like, int8 g128, bf16 scales, bf16 out; max relative error 1e-2 (relative to
-    the largest output) against the f64 product. Weights N(0, 0.02) from the synthetic generator."""
-    print(f"case k={k} n={n} m={m_tokens}", flush=True)
-    wbits = o.synth(11, 100 + n + k, n * k)
-    codes, scales = o.quantize(wbits, n, k, 8, 128)
+@pytest.mark.parametrize("bits", [8, 4])
+def test_decode_shapes_bf16_layout_within_the_north_star_tolerance(gpu, k, n, m_tokens, bits):
+    """Config 1: bf16 activations N(0,1)-like, int8 (or int4) g128, bf16 scales, bf16 out; max relative error 1e-2
+    (relative to the largest output) against the f64 product. Weights N(0, 0.02) from the synthetic generator."""
+    print(f"case bits={bits} k={k} n={n} m={m_tokens}", flush=True)
+    codes, scales = config1_matrix(k, n, bits)
     sbf = o.f32_to_bf16_rne(scales)
     s32 = o.bf16_to_f32(sbf)
     x = o.f32_to_bf16_rne(values_fast(m_tokens * k, 99) * np.float32(1.7))
     xf = o.bf16_to_f32(x).astype(np.float64).reshape(m_tokens, k)
-    w = gpu.upload_quantized(n, k, 8, 128, codes, sbf, bf16_scales=True)
+    w = gpu.upload_quantized(n, k, bits, 128, codes, sbf, bf16_scales=True)
     xb = gpu.typed(1, host=x)
     out = gpu.typed(1, m_tokens * n)
     gpu.matmul_quant_bf16(w, xb, m_tokens, out)
     got = o.bf16_to_f32(gpu.download_typed(out)).astype(np.float64).reshape(m_tokens, n)
-    # f64 reference in row blocks to bound host memory
+    # f64 reference in row blocks to bound host memory; int4: the even column in the low nibble, stored + 8
+    # (tensor/src/quant.rs:218-229)
     exp = np.zeros((m_tokens, n))
-    cview = codes.reshape(n, k).view(np.int8)
     sv = s32.reshape(n, k // 128)
+    if bits == 8:
+        cview = codes.reshape(n, k).view(np.int8)
+    else:
+        cview = codes.reshape(n, k // 2)
     for r0 in range(0, n, 8192):
         r1 = min(n, r0 + 8192)
-        deq = cview[r0:r1].astype(np.float64).reshape(r1 - r0, k // 128, 128) * sv[r0:r1, :, None]
+        if bits == 8:
+            c = cview[r0:r1].astype(np.float64)
+        else:
+            packed = cview[r0:r1]
+            c = np.empty((r1 - r0, k), np.float64)
+            c[:, 0::2] = (packed & 0x0F).astype(np.float64) - 8.0
+            c[:, 1::2] = (packed >> 4).astype(np.float64) - 8.0
+        deq = c.reshape(r1 - r0, k // 128, 128) * sv[r0:r1, :, None]
         exp[:, r0:r1] = xf @ deq.reshape(r1 - r0, k).T
     rel = np.abs(got - exp).max() / np.abs(exp).max()
     assert rel <= 1e-2, rel

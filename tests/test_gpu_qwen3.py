@@ -110,7 +110,7 @@ def test_a_prompt_longer_than_a_chunk_matches_the_oracle(gpu, fmt):
 
 
 @pytest.mark.parametrize("name", ["mini_f16kv", "1.7b"])
-def test_prompt_attention_on_the_matrix_cores_equals_the_vector_path(gpu, name, monkeypatch):
+def test_prompt_attention_on_the_matrix_cores_equals_the_vector_path(gpu, name):
     """The f16-cache prompt pass with its attention on the matrix cores (q and P split into two f16 parts each)
     against the same pass on the vector-ALU attention: the logits agree to f32 accuracy. 1300 tokens: chunks of 512,
     512 and 276, the last one's rows split over two spans of 1024 positions and merged."""
@@ -119,13 +119,12 @@ def test_prompt_attention_on_the_matrix_cores_equals_the_vector_path(gpu, name, 
     prompt = o.synth_prompt(g["seed"] + 3, 1300, shape["vocab"]).tolist()
     model = Qwen3(gpu, shape, seed=g["seed"])
     out = []
-    for fa in ("0", "1"):
-        if fa == "1":
-            monkeypatch.setenv("MARIN_NO_FA", "1")
-        else:
-            monkeypatch.delenv("MARIN_NO_FA", raising=False)
-        out.append(model.forward(prompt, model.new_cache(len(prompt) + 1, m.KvFormat.F16)))
-    monkeypatch.delenv("MARIN_NO_FA", raising=False)
+    try:
+        for fast in (True, False):  # Gpu::set_fast_attention (attention.rs:81-86)
+            gpu.set_fast_attention(fast)
+            out.append(model.forward(prompt, model.new_cache(len(prompt) + 1, m.KvFormat.F16)))
+    finally:
+        gpu.set_fast_attention(True)
     assert np.abs(out[0] - out[1]).max() <= 2e-4 * (1 + np.abs(out[1]).max())
 
 
@@ -236,3 +235,38 @@ def test_a_packed_artifact_loads_the_same_model_as_quantizing_on_load(gpu, tmp_p
     a = packed.forward(prompt, packed.new_cache(64))
     b = direct.forward(prompt, direct.new_cache(64))
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_a_4096_token_prompt_at_8b_widths_matches_the_golden(gpu):
+    """Config 3's prompt at its own length on an 8B-width model of reduced depth (2 layers): the 4096-token prefill
+    with an f16 cache runs in 512-token passes on the matrix cores (rows past 1024 positions split over spans and
+    merged), then 64 greedy tokens on the decode path. Tokens equal the oracle's until a step whose top-1/top-2 gap
+    is a near tie; the first step's top-5 logits agree within f16-cache accuracy."""
+    g = golden("8b_long")
+    shape = g["shape"]
+    model = Qwen3(gpu, shape, seed=g["seed"])
+    steps = len(g["tokens"])
+    cache = model.new_cache(len(g["prompt"]) + steps + 1, m.KvFormat.F16)
+    toks = model.generate(g["prompt"], steps, cache)
+    assert agree_until_a_near_tie(toks.tolist(), g["tokens"], g["gaps"]) >= steps // 2
+    cache = model.new_cache(len(g["prompt"]) + 2, m.KvFormat.F16)
+    logits = model.forward(g["prompt"], cache)
+    ids, vals = g["top_ids"][0], np.array(g["top_vals"][0])
+    assert np.abs(logits[ids] - vals).max() <= 1e-3 * (1 + np.abs(vals).max())
+
+
+def test_batch_8_decode_at_8b_widths_matches_the_golden(gpu):
+    """Config 3's batch 8 at 8B widths (3 layers): eight prompts of different lengths decoded together, every
+    product over the batch on the batch kernels of the 8B shapes; each sequence gets the oracle's greedy tokens
+    (tests/golden/qwen3_8b_batch_greedy.json), or first differs at a near tie."""
+    g = golden("8b_batch")
+    shape, seqs, steps = g["shape"], g["sequences"], g["steps"]
+    model = Qwen3(gpu, shape, seed=g["seed"])
+    b = model.new_batch(len(seqs), max(len(s["prompt"]) for s in seqs) + steps + 1)
+    for i, s in enumerate(seqs):
+        b.prefill(i, s["prompt"])
+    got = b.decode(steps)
+    compared = 0
+    for i, s in enumerate(seqs):
+        compared += agree_until_a_near_tie(got[i].tolist(), s["tokens"], s["gaps"])
+    assert compared >= len(seqs) * steps // 2
