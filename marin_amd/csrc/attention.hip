@@ -123,7 +123,7 @@ __device__ __forceinline__ void store_kv(uint8_t *row, int e, float x) {
 // One head's RMSNorm(weight) + RoPE inputs held by one wave: lane i takes the pairs (i, i + hd/2), i < hd/2 (hd
 // even, at most 256), with their norm weights and RoPE frequencies.
 struct HeadIn {
-    float a[2], b[2], wa[2], wb[2], f[2];
+    float a[2], b[2], wa[2], wb[2], f[2], s[2];  // f: the frequency, or with a cos/sin table the cosine (s the sine)
 };
 
 __device__ __forceinline__ HeadIn load_head(const float *__restrict__ src, const float *__restrict__ w,
@@ -490,10 +490,12 @@ __global__ __launch_bounds__(64 * NW) void attention_split(
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     };
-    // Counts the workgroup in; true for the last of `n`.
+    // Counts the workgroup in; true for the last of `n`. The count is an acquire-release at agent scope: the
+    // workgroup's record stores (acknowledged above) are released with it, and the last arriver's merge loads are
+    // ordered after it, whatever the cache bits of those loads and stores.
     auto arrive = [&](uint32_t *counter, int n) {
         if (threadIdx.x == 0)
-            last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(n - 1);
+            last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(n - 1);
         __syncthreads();
         return last_s != 0;
     };
@@ -568,16 +570,93 @@ __global__ __launch_bounds__(64 * NW) void attention_split(
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// One-token decode attention (every sequence adds one position), built for latency.
+// One-token decode attention (every sequence adds one position): one launch, merge included.
 //
-// grid: x = chunk of the context, y = kv head, z = sequence; 4 waves. A workgroup takes `chunk` positions of one kv
-// head for all `group` query heads of it (R >= group rows). Lanes work in groups of LPP per position with 8 head
-// values a lane, so a wave covers 64 / LPP positions per step; the workgroup's steps are issued as one burst of loads
-// (up to U per lane for keys and as many for values) right after its page addresses are known, so a chunk costs one
-// memory round trip. With FUSE, q and the new key get RMSNorm + RoPE in the kernel; the workgroup whose chunk holds
-// the new position takes that key and value from LDS (rounded to the cache format, exactly as stored) and stores them
-// into the cache without waiting for the store. Chunks write a record (max, sum, weighted values) per row with
-// agent-coherent stores; the last chunk of a (sequence, kv head) to arrive merges all of them in chunk order.
+// grid: x = chunk of the context, y = kv head, z = sequence; 4 waves. A workgroup takes `chunk` = U steps of
+// positions of one kv head for all `group` query heads of it (R >= group rows). Lanes work in groups of LPP per
+// position with 8 head values a lane (a wave covers 64 / LPP positions per step). Every lane reads the page address of
+// each of its positions itself and then issues all of its key and value rows at once, so a chunk costs two dependent
+// memory round trips and nothing waits on a barrier before the rows are in flight.
+//  - With FUSE the query heads (and, in the workgroup whose chunk holds the new position, the new key and value) are
+//    loaded before anything else and get RMSNorm + RoPE while the rows are in flight; that workgroup takes the new key
+//    and value from LDS (rounded to the cache format exactly as stored) and stores them into the cache last.
+//  - Scores and weights are in the log2 domain (the host folds log2(e) into `scale`). A lane group keeps its
+//    positions' (max, sum, weighted values); the groups of a wave combine through lane shuffles, the waves through
+//    LDS, all in a fixed order.
+//  - More than one chunk: each writes a record (max, sum, weighted values) per row with agent-coherent stores, waits
+//    for them, and counts itself in on the (sequence, kv head)'s counter; the last to arrive reads every record of its
+//    rows and merges them in chunk order, so the result does not depend on arrival order. Its loads are
+//    agent-coherent too: on gfx950 a store or load with the device scope bit (sc1) goes through to the device's
+//    coherence point rather than one die's L2, so the records need no cache write-back or invalidation, and the
+//    counter's atomic is issued only after the record stores have been acknowledged (s_waitcnt vmcnt(0)).
+// Values of lane `lane` and its partner `o` lanes away (o a power of two), as (lower lane's, upper lane's), the same in
+// both lanes. Partners 16 and 32 lanes away use the gfx950 row swaps (VALU, no LDS round trip).
+__device__ __forceinline__ void pair_lanes(float v, int o, int lane, float &lo, float &hi) {
+    if (o == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else if (o == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        const float other = __shfl_xor(v, o);
+        const bool upper = (lane & o) != 0;
+        lo = upper ? other : v;
+        hi = upper ? v : other;
+    }
+}
+
+// load_head with the RoPE angle's cosine and sine read from a table row (pairs for i = 0 .. hd/2 - 1) instead of
+// the frequency; finish_head_cs applies them.
+__device__ __forceinline__ HeadIn load_head_cs(const float *__restrict__ src, const float *__restrict__ w,
+                                               const float2 *__restrict__ cs, int hd, int lane) {
+    const int half = hd / 2;
+    HeadIn h;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = lane + 64 * k;
+        const bool in = i < half;
+        h.a[k] = in ? src[i] : 0.0f;
+        h.b[k] = in ? src[i + half] : 0.0f;
+        h.wa[k] = in ? w[i] : 0.0f;
+        h.wb[k] = in ? w[i + half] : 0.0f;
+        const float2 c = in ? cs[i] : make_float2(1.0f, 0.0f);
+        h.f[k] = c.x;
+        h.s[k] = c.y;
+    }
+    return h;
+}
+
+__device__ __forceinline__ void finish_head_cs(const HeadIn &h, int hd, float eps, int lane, float a[2], float b[2]) {
+    const int half = hd / 2;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) s += h.a[k] * h.a[k] + h.b[k] * h.b[k];
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const float scale = 1.0f / sqrtf(s / (float)hd + eps);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = lane + 64 * k;
+        a[k] = b[k] = 0.0f;
+        if (i >= half) continue;
+        const float x = h.a[k] * scale * h.wa[k], y = h.b[k] * scale * h.wb[k];
+        const float cs = h.f[k], sn = h.s[k];
+        a[k] = x * cs - y * sn;
+        b[k] = y * cs + x * sn;
+    }
+}
+
+#ifndef ATTN_MERGE_KERNEL
+#define ATTN_MERGE_KERNEL 1
+#endif
+constexpr int DEC_NW = 4;           // waves per workgroup
+constexpr int DEC_MAX_SPLITS = 64;  // chunks the last workgroup merges (a lane of one wave each)
+
+// Steps of key/value loads per lane a workgroup may take (the burst held in registers).
+template <int F, int R>
+__host__ __device__ constexpr int dec_umax() { return F == MARIN_KV_F32 ? (R <= 4 ? 8 : 4) : (R <= 4 ? 16 : 8); }
 
 // Eight values of a new key or value row in the cache's storage format (store_kv's rounding).
 template <int F>
@@ -609,25 +688,110 @@ __device__ __forceinline__ Raw8<F> to_raw(const float *v) {
     return r;
 }
 
-constexpr int DEC_NW = 4;        // waves per workgroup
-constexpr int DEC_MAX_SPLITS = 64;  // chunks merged by the last workgroup
+// Merges the records of `used` chunks for the `group` rows of one (sequence, kv head) and writes the rows' outputs.
+// One memory round trip: the value threads (a thread per (row, 4 values, share of the records), up to VR records
+// each) issue their loads, then a wave per row loads the records' (max, sum), a lane per record; the row's maximum,
+// weights and weighted sum are lane reductions in a fixed pattern, so the result does not depend on which chunk
+// finished last. LDS: wt_s [R][DEC_MAX_SPLITS] weights, lsum_s [R], sh_s 3 * group * hd floats.
+template <bool BF16IO, int R, int NW>
+__device__ __forceinline__ void merge_records(__amdgpu_buffer_rsrc_t prs, int rec0, int rec_row, int rec_bytes,
+                                              int hd, int group, int used, float (*wt_s)[DEC_MAX_SPLITS],
+                                              float *lsum_s, float *sh_s, void *out, size_t out_row0) {
+    constexpr int NT = 64 * NW, QPW = (R + NW - 1) / NW;
+    constexpr int SC1 = 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    auto rec_off = [&](int r, int k) { return rec0 + r * rec_row + k * rec_bytes; };
+    auto write_out = [&](int r, int e, float v) {
+        const size_t at = (out_row0 + r) * hd + e;
+        if constexpr (BF16IO) {
+            const unsigned u = __float_as_uint(v);
+            reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        } else {
+            reinterpret_cast<float *>(out)[at] = v;
+        }
+    };
+    constexpr int VR = 16;                 // records' values a thread holds
+    const int c4n = hd / 4;
+    const int items = group * c4n;         // (row, 4 values)
+    const int shares = max(1, min(NT / items, 4));
+    const int per = (used + shares - 1) / shares;  // records of one share
+    const int item = (int)threadIdx.x % items, share = (int)threadIdx.x / items;
+    const bool valuer = share < shares;
+    const int r = item / c4n, e4 = item - r * c4n;
+    const int k_lo = share * per, k_hi = min(used, k_lo + per);
+    u32x4 vv[VR];
+    auto value_burst = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < VR; ++j) {
+            const int k = min(k0 + j, max(k_hi - 1, 0));
+            vv[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, rec_off(r, k) + 16 * (1 + e4), 0, SC1);
+        }
+    };
+    if (valuer) value_burst(k_lo);
+    {
+        u32x4 hdr[QPW];
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int rr = min(wave + j * NW, group - 1);
+            hdr[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, rec_off(rr, min(lane, used - 1)), 0, SC1);
+        }
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int rr = wave + j * NW;
+            const float mk = lane < used ? __uint_as_float(hdr[j][0]) : -INFINITY;
+            const float lk = lane < used ? __uint_as_float(hdr[j][1]) : 0.0f;
+            float mx = mk;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            const float wt = mk == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mk - mx);
+            float lsum = lk * wt;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+            if (rr < group) {
+                wt_s[rr][lane] = wt;
+                if (lane == 0) lsum_s[rr] = lsum;
+            }
+        }
+    }
+    __syncthreads();
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (valuer) {
+        for (int k0 = k_lo; k0 < k_hi; k0 += VR) {
+            if (k0 != k_lo) value_burst(k0);
+#pragma unroll
+            for (int j = 0; j < VR; ++j) {
+                const int k = k0 + j;
+                const float wt = k < k_hi ? wt_s[r][k] : 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) a[t] += __uint_as_float(vv[j][t]) * wt;
+            }
+        }
+    }
+    // the shares' sums meet in share order
+    if (valuer && share > 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sh_s[((share - 1) * items + item) * 4 + t] = a[t];
+    }
+    __syncthreads();
+    if (valuer && share == 0) {
+        for (int sh = 1; sh < shares; ++sh)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[t] += sh_s[((sh - 1) * items + item) * 4 + t];
+        const float lsum = lsum_s[r];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) write_out(r, 4 * e4 + t, a[t] / lsum);
+    }
+}
 
-// Steps of key/value loads in flight per lane: one workgroup per compute unit leaves the registers for deeper bursts
-// when the group (rows) is small.
-template <int F, int R>
-__host__ __device__ constexpr int dec_umax() { return F == MARIN_KV_F32 ? (R <= 4 ? 6 : 4) : (R <= 4 ? 12 : 8); }
-
-template <int F, int LPP, bool BF16IO, int R, bool FUSE>
+template <int F, int LPP, bool BF16IO, int R, bool FUSE, int U>
 __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const void *__restrict__ qv, AttnFuse fuse, const uint64_t *__restrict__ tables, size_t table_stride,
     const uint32_t *__restrict__ ctx_lens, KvGeom geom, int heads, int kv_heads, int chunk, int splits, float scale,
     float *__restrict__ part, int part_bytes, uint32_t *__restrict__ counters, void *__restrict__ out) {
     constexpr int NW = DEC_NW, NT = 64 * NW;
-    constexpr int HMAX = 8 * LPP;          // head values covered by the lanes of one position
-    constexpr int PPW = 64 / LPP;          // positions per wave step
-    constexpr int STEP = NW * PPW;         // positions per workgroup step
-    constexpr int U = dec_umax<F, R>();
-    constexpr int MAXPG = U * STEP + 1;    // page addresses of one chunk (pages of at least one position)
+    constexpr int HMAX = 8 * LPP;  // head values covered by the lanes of one position
+    constexpr int PPW = 64 / LPP;  // positions per wave step
+    constexpr int STEP = NW * PPW; // positions per workgroup step
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int slot = lane / LPP, sub = lane % LPP;
     const int hd = (int)geom.head_dim;
@@ -646,74 +810,78 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const uint64_t *table = tables + (size_t)b * table_stride;
     const int newpos = ctx - 1;
     const bool owns_new = FUSE && newpos >= first && newpos < first + count;
-    ATT_T(0);
 
-    __shared__ uint64_t pages_s[MAXPG];
+    ATT_T(0);
     __shared__ float q_s[R][HMAX];
     __shared__ float new_s[2][HMAX];  // the new key (normalized and rotated) and value
-    __shared__ float red_acc[NW * PPW][R][HMAX];
-    __shared__ float red_ml[NW * PPW][R][2];
-    __shared__ float ml_s[R][2];
+    __shared__ float wm_s[NW][R], wl_s[NW][R];
+    __shared__ float wacc_s[NW][R][HMAX];
+    __shared__ float hm_s[R][DEC_MAX_SPLITS], hl_s[R][DEC_MAX_SPLITS];
+    __shared__ int last_s;
 
-    // ---- one burst: the query inputs (with FUSE, the raw q heads of this kv head and, in the workgroup that owns the
-    // new position, the raw new key and value), issued first so they are not queued behind other workgroups' rows,
-    // then the page addresses
+    // ---- 1. page addresses of this lane's positions (clamped to the chunk's last), first of all loads
+    uint64_t pg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int p = first + min(wave * PPW + slot + u * STEP, count - 1);
+        pg[u] = table[p >> geom.page_shift];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- 2. the query inputs (FUSE: raw q heads with the cos/sin of the new position, and the raw new key and value
+    // where this chunk holds them), issued behind the page addresses so waiting for those does not wait for these
     constexpr int QPW = (R + NW - 1) / NW;  // q heads per wave
-    // with FUSE, sequence b's q | k | v row (one token each) is row b of the fused rows
     const float *fq = FUSE ? fuse.qkv + (size_t)b * (heads + 2 * kv_heads) * hd : nullptr;
     HeadIn qin[QPW], kin;
     float vin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float q[R][8];
     if constexpr (FUSE) {
 #pragma unroll
         for (int j = 0; j < QPW; ++j) {
             const int r = wave + j * NW;
-            if (r < group) qin[j] = load_head(fq + (size_t)(kvh * group + r) * hd, fuse.q_norm, fuse.freq, hd, lane);
+            if (r < group) qin[j] = load_head_cs(fq + (size_t)(kvh * group + r) * hd, fuse.q_norm, fuse.rope + (size_t)newpos * (hd / 2), hd, lane);
         }
         if (owns_new && wave == NW - 1) {
-            kin = load_head(fq + (size_t)(heads + kvh) * hd, fuse.k_norm, fuse.freq, hd, lane);
+            kin = load_head_cs(fq + (size_t)(heads + kvh) * hd, fuse.k_norm, fuse.rope + (size_t)newpos * (hd / 2), hd, lane);
             const float *vsrc = fq + (size_t)(heads + kv_heads + kvh) * hd;
 #pragma unroll
             for (int k = 0; k < 4; ++k) vin[k] = lane + 64 * k < hd ? vsrc[lane + 64 * k] : 0.0f;
         }
     } else {
-        for (int i = threadIdx.x; i < group * hd; i += NT) {
-            const int r = i / hd, e = i % hd;
-            const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
-            if constexpr (BF16IO) q_s[r][e] = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(qv)[at]);
-            else q_s[r][e] = reinterpret_cast<const float *>(qv)[at];
+        // this lane's 8 values of every q head of the kv head, straight into registers
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int rr = min(r, group - 1);
+            const size_t at = ((size_t)b * heads + kvh * group + rr) * hd + dl;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float v = BF16IO ? bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(qv)[at + i])
+                                       : reinterpret_cast<const float *>(qv)[at + i];
+                q[r][i] = (r < group && d + i < hd) ? v : 0.0f;
+            }
         }
     }
-    const int page0 = first >> geom.page_shift;
-    const int npages = ((first + count - 1) >> geom.page_shift) - page0 + 1;
-    for (int i = threadIdx.x; i < npages; i += NT) pages_s[i] = table[page0 + i] + head_off;
-    __syncthreads();
-    ATT_T(1);
+    __builtin_amdgcn_sched_barrier(0);  // the query loads stay ahead of the row loads
 
-    // ---- every key and value row of the chunk in flight at once (clamped positions past the chunk's end)
-    auto row_ptr = [&](int which, int p) {
-        const uint32_t pos = (uint32_t)(first + p);
-        return reinterpret_cast<const uint8_t *>(pages_s[(pos >> geom.page_shift) - page0] +
-                                                 (which ? geom.value_offset : 0) + (uint64_t)(pos & pmask) * hd * es);
-    };
-    const int steps = (count + STEP - 1) / STEP;  // <= U
-    // Every step's rows are loaded unconditionally (positions past the chunk clamped to its last one): a load under
-    // a branch would make the wait for the query inputs below also wait for every row. Rows of positions past the
-    // chunk are zeroed when used, so their weight 0 never meets a non-finite value.
+    // ---- 3. every key and value row of the chunk
     Raw8<F> kr[U], vr[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int p = min(wave * PPW + slot + u * STEP, count - 1);
-        load_raw<F, true>(row_ptr(0, p), dl, hd, kr[u]);
-        load_raw<F, true>(row_ptr(1, p), dl, hd, vr[u]);
+        const uint32_t p = (uint32_t)(first + min(wave * PPW + slot + u * STEP, count - 1));
+        const uint8_t *row = reinterpret_cast<const uint8_t *>(pg[u] + head_off + (uint64_t)(p & pmask) * hd * es);
+        load_raw<F, true>(row, dl, hd, kr[u]);
+        load_raw<F, true>(row + geom.value_offset, dl, hd, vr[u]);
     }
-    // ---- with FUSE: q and the new key normalized and rotated while the rows are in flight
+    __builtin_amdgcn_sched_barrier(0);
+    ATT_T(1);
+
+    // ---- 4. FUSE: q and the new key normalized and rotated while the rows are in flight
     if constexpr (FUSE) {
 #pragma unroll
         for (int j = 0; j < QPW; ++j) {
             const int r = wave + j * NW;
             if (r < group) {
                 float a2[2], b2[2];
-                finish_head(qin[j], (uint32_t)newpos, hd, fuse.eps, lane, a2, b2);
+                finish_head_cs(qin[j], hd, fuse.eps, lane, a2, b2);
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
                     const int i = lane + 64 * k;
@@ -726,7 +894,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
         }
         if (owns_new && wave == NW - 1) {
             float a2[2], b2[2];
-            finish_head(kin, (uint32_t)newpos, hd, fuse.eps, lane, a2, b2);
+            finish_head_cs(kin, hd, fuse.eps, lane, a2, b2);
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int i = lane + 64 * k;
@@ -740,15 +908,14 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
                 if (lane + 64 * k < hd) new_s[1][lane + 64 * k] = vin[k];
         }
         __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[r][i] = (r < group && d + i < hd) ? q_s[r][d + i] : 0.0f;
     }
-    ATT_T(2);
-    float q[R][8];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[r][i] = (r < group && d + i < hd) ? q_s[r][d + i] : 0.0f;
 
-    // ---- scores, then one softmax pass over this lane group's positions
+    ATT_T(2);
+    // ---- 5. scores, then one softmax pass over this lane group's positions
     float sc[R][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -763,7 +930,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
             kr[u] = to_raw<F>(kn);
             vr[u] = to_raw<F>(vn);
         }
-        const bool valid = u < steps && p < count;
+        const bool valid = p < count;
         if (!valid) {
 #pragma unroll
             for (int j = 0; j < (F == MARIN_KV_F32 ? 2 : 1); ++j) kr[u].w[j] = vr[u].w[j] = (u32x4){0u, 0u, 0u, 0u};
@@ -797,52 +964,60 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
             }
         }
     }
-    // ---- every (wave, position slot) leaves its maximum, sum and weighted values in LDS; the workgroup combines
-    // the NS = NW * PPW partials in a fixed order
-    ATT_T(3);
-    constexpr int NS = NW * PPW;
-    const int ps = wave * PPW + slot;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (d + i < hd) red_acc[ps][r][d + i] = acc[r][i];
-        if (sub == 0) {
-            red_ml[ps][r][0] = mrow[r];
-            red_ml[ps][r][1] = lrow[r];
-        }
-    }
-    __syncthreads();
-    // the partials' weights: a thread per (row, partial), the row's maximum over its partials by lane shuffles
-    // (NS consecutive lanes, NS a power of two <= 64)
-    {
-        const int r = threadIdx.x / NS, w = threadIdx.x % NS;
-        const bool on = r < group;
-        const float mw = on ? red_ml[w][r][0] : -INFINITY;
-        float mn = mw;
-#pragma unroll
-        for (int o = 1; o < NS; o <<= 1) mn = fmaxf(mn, __shfl_xor(mn, o));
-        const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mn);
-        float l = on ? red_ml[w][r][1] * wt : 0.0f;
-#pragma unroll
-        for (int o = 1; o < NS; o <<= 1) l += __shfl_xor(l, o);
-        __syncthreads();  // every thread has read red_ml before it is overwritten with weights
-        if (on) red_ml[w][r][0] = wt;
-        if (on && w == 0) {
-            ml_s[r][0] = mn;
-            ml_s[r][1] = l;
-        }
-    }
-    __syncthreads();
-    for (int o = threadIdx.x; o < group * hd; o += NT) {
-        const int r = o / hd, e = o % hd;
-        float a = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NS; ++w) a += red_acc[w][r][e] * red_ml[w][r][0];
-        q_s[r][e] = a;  // the workgroup's weighted values (q is in registers)
-    }
-    __syncthreads();
 
+    ATT_T(3);
+    // ---- 6. the lane groups of a wave combined pairwise (partners LPP, 2 LPP, ... lanes apart; both lanes of a pair
+    // compute the same lower-then-upper combination), then the waves through LDS; each step rescales both sides to
+    // the larger maximum
+#pragma unroll
+    for (int o = LPP; o < 64; o <<= 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float m0, m1, l0, l1;
+            pair_lanes(mrow[r], o, lane, m0, m1);
+            pair_lanes(lrow[r], o, lane, l0, l1);
+            const float mn = fmaxf(m0, m1);
+            const float fa = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - mn);
+            const float fb = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mn);
+            lrow[r] = l0 * fa + l1 * fb;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float a0, a1;
+                pair_lanes(acc[r][i], o, lane, a0, a1);
+                acc[r][i] = a0 * fa + a1 * fb;
+            }
+            mrow[r] = mn;
+        }
+    }
+    if (slot == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wacc_s[wave][r][d + i] = acc[r][i];
+            if (sub == 0) {
+                wm_s[wave][r] = mrow[r];
+                wl_s[wave][r] = lrow[r];
+            }
+        }
+    }
+    __syncthreads();
+    ATT_T(4);
+    // the workgroup's (max, sum, weighted values) of row r, value e: the waves in order
+    auto combine = [&](int r, int e, float &m_out, float &l_out) {
+        float mn = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mn = fmaxf(mn, wm_s[w][r]);
+        float a = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float f = wm_s[w][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(wm_s[w][r] - mn);
+            a += wacc_s[w][r][e] * f;
+            l += wl_s[w][r] * f;
+        }
+        m_out = mn;
+        l_out = l;
+        return a;
+    };
     auto write_out = [&](int r, int e, float v) {
         const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
         if constexpr (BF16IO) {
@@ -852,8 +1027,9 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
             reinterpret_cast<float *>(out)[at] = v;
         }
     };
-    // the new key and value, stored for later steps (this launch read them from LDS); stored last, as a store under
-    // a branch earlier on would make the waits for the rows drain every load in flight
+
+    // the new key and value, stored for later steps (this launch took them from LDS); stored here, after every
+    // load of the chunk has been waited for, so the store cannot make those waits drain anything
     if (owns_new && wave == NW - 1) {
         const uint64_t page = table[newpos >> geom.page_shift] + head_off + (uint64_t)(newpos & pmask) * hd * es;
         for (int i = lane; i < hd; i += 64) {
@@ -862,147 +1038,76 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
         }
     }
     if (used == 1) {
-        for (int o = threadIdx.x; o < group * hd; o += NT) write_out(o / hd, o % hd, q_s[o / hd][o % hd] / ml_s[o / hd][1]);
+        for (int o = threadIdx.x; o < group * hd; o += NT) {
+            float m, l;
+            const float a = combine(o / hd, o % hd, m, l);
+            write_out(o / hd, o % hd, a / l);
+        }
         return;
     }
 
-    // ---- record of this chunk (max, sum, weighted values per row); attention_decode_merge combines them
+    // ---- 7. this chunk's record per row: [max, sum, 0, 0, values, pad], 16-byte agent-coherent stores
     const int RS = rec_floats(hd);
-    float *rec = part + (((size_t)b * heads + kvh * group) * splits + split) * (size_t)RS;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, part_bytes, 0x00020000);
+    constexpr int SC1 = 16;  // the device-scope bit of the cache policy
+    auto rec_off = [&](int r, int sp) {
+        return (int)(((((size_t)b * heads + kvh * group + r) * splits) + sp) * (size_t)RS * 4);
+    };
     for (int o = threadIdx.x; o < group * (RS / 4); o += NT) {
         const int r = o / (RS / 4), c4 = o % (RS / 4);
-        float4 v;
+        u32x4 v;
+        float m, l;
         if (c4 == 0) {
-            v = make_float4(ml_s[r][0], ml_s[r][1], 0.0f, 0.0f);
+            (void)combine(r, 0, m, l);
+            v = (u32x4){__float_as_uint(m), __float_as_uint(l), 0u, 0u};
         } else {
-            const int e = 4 * (c4 - 1);
-            v = make_float4(e < hd ? q_s[r][e] : 0.0f, e + 1 < hd ? q_s[r][e + 1] : 0.0f,
-                            e + 2 < hd ? q_s[r][e + 2] : 0.0f, e + 3 < hd ? q_s[r][e + 3] : 0.0f);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * (c4 - 1) + j;
+                v[j] = e < hd ? __float_as_uint(combine(r, e, m, l)) : 0u;
+            }
         }
-        *reinterpret_cast<float4 *>(rec + (size_t)r * splits * RS + 4 * c4) = v;
+        __builtin_amdgcn_raw_buffer_store_b128(v, prs, rec_off(r, split) + 16 * c4, 0, ATTN_MERGE_KERNEL ? 0 : SC1);
     }
-    ATT_T(6);
+#if ATTN_MERGE_KERNEL
+    return;  // attention_decode_merge combines the records after this launch
+#endif
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every record store acknowledged before counting in
+    __syncthreads();
+    uint32_t *counter = counters + (size_t)b * kv_heads + kvh;
+    if (threadIdx.x == 0)
+        last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(used - 1);
+    __syncthreads();
+    if (!last_s) return;
+
+    ATT_T(5);
+    // ---- 8. the last chunk to arrive merges every record of its rows
+    merge_records<BF16IO, R, NW>(prs, rec_off(0, 0), rec_off(1, 0) - rec_off(0, 0), RS * 4, hd, group, used, hm_s,
+                                 &hl_s[0][0], &wacc_s[0][0][0], out, (size_t)b * heads + kvh * group);
+    ATT_T(7);
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The chunks of one (sequence, kv head) combined with log-sum-exp weights, in chunk order: a workgroup per
-// (kv head, sequence). Chunk weights are computed a lane per (row, chunk) with the row's chunks in consecutive lanes
-// (a power-of-two span P, so the row's maximum and sum are lane shuffles); the weighted values are summed a thread
-// per (row, 4 values, half of the chunks), every record word of the thread loaded in one burst.
+// The chunk records of each (sequence, kv head) merged after attention_decode: a workgroup per (kv head, sequence).
 template <bool BF16IO, int R>
-__global__ __launch_bounds__(256) void attention_decode_merge(const float *__restrict__ part,
-                                                              const uint32_t *__restrict__ ctx_lens, int hd,
-                                                              int heads, int kv_heads, int chunk, int splits,
-                                                              void *__restrict__ out) {
-    constexpr int NT = 256;
+__global__ __launch_bounds__(64 * DEC_NW) void attention_decode_merge(const float *__restrict__ part, int part_bytes,
+                                                                      const uint32_t *__restrict__ ctx_lens, int hd,
+                                                                      int heads, int kv_heads, int chunk, int splits,
+                                                                      void *__restrict__ out) {
     __shared__ float wt_s[R][DEC_MAX_SPLITS];
-    __shared__ float l_s[R];
-    __shared__ float half_s[R][256];
+    __shared__ float lsum_s[R];
+    __shared__ float sh_s[3 * R * 256];
     const int kvh = blockIdx.x, b = blockIdx.y;
     const int group = heads / kv_heads;
     const int ctx = (int)ctx_lens[b];
     const int used = (ctx + chunk - 1) / chunk;
     if (used <= 1) return;  // a context of one chunk was written by attention_decode itself
     const int RS = rec_floats(hd);
-    const float *rec0 = part + ((size_t)b * heads + kvh * group) * splits * (size_t)RS;
-    auto write_out = [&](int r, int e, float v) {
-        const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
-        if constexpr (BF16IO) {
-            const unsigned u = __float_as_uint(v);
-            reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-        } else {
-            reinterpret_cast<float *>(out)[at] = v;
-        }
-    };
-    // chunk headers: lane per (row, chunk) over a span P (power of two >= used, <= 64)
-    int P = 1;
-    while (P < used) P <<= 1;
-    float2 hdr[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = threadIdx.x + h * NT, r = i / P, k = i % P;
-        hdr[h] = (r < group && k < used) ? *reinterpret_cast<const float2 *>(rec0 + ((size_t)r * splits + k) * RS)
-                                         : make_float2(-INFINITY, 0.0f);
-    }
-    // weighted values: a thread per (row, 4 values, share of the chunks): chunk k of share h is h + halves * j; one
-    // unrolled burst of clamped loads per pass of J chunks, the first issued before the weights are known
-    constexpr int J = 16;
-    const int c4n = (hd + 3) / 4;
-    const int pairs = group * c4n;
-    const int halves = pairs * 2 <= NT ? 2 : 1;
-    const int per = (used + halves - 1) / halves;
-    const int passes = (per + J - 1) / J;
-    float4 v[J];
-    auto burst = [&](int col, int hf, int pass) {
-        const int r = col / c4n, e4 = col - r * c4n;
-        const float *base = rec0 + (size_t)r * splits * RS + 4 + 4 * e4;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int k = min(hf + halves * (pass * J + j), used - 1);
-            v[j] = *reinterpret_cast<const float4 *>(base + (size_t)k * RS);
-        }
-    };
-    auto accumulate = [&](int col, int hf, int pass, float a[4]) {
-        const int r = col / c4n;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int k = hf + halves * (pass * J + j);
-            const float w = k < used ? wt_s[r][k] : 0.0f;
-            a[0] += v[j].x * w;
-            a[1] += v[j].y * w;
-            a[2] += v[j].z * w;
-            a[3] += v[j].w * w;
-        }
-    };
-    const int hf0 = (int)threadIdx.x / pairs;
-    const int col0 = (int)threadIdx.x - hf0 * pairs;
-    const bool active = hf0 < halves;  // threads of the first column sweep
-    if (active) burst(col0, hf0, 0);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = threadIdx.x + h * NT, rr = i / P, k = i % P;
-        float m = hdr[h].x;
-        for (int o = 1; o < P; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float w = hdr[h].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(hdr[h].x - m);
-        float l = hdr[h].y * w;
-        for (int o = 1; o < P; o <<= 1) l += __shfl_xor(l, o);
-        if (rr < group && k < used) wt_s[rr][k] = w;
-        if (rr < group && k == 0) l_s[rr] = l;
-    }
-    __syncthreads();
-    if (halves == 2) {
-        // pairs <= NT / 2: every column has both shares; the second share's sums meet the first's in LDS
-        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int r = col0 / c4n, e4 = col0 - r * c4n;
-        if (active) {
-            for (int pass = 0; pass < passes; ++pass) {
-                if (pass) burst(col0, hf0, pass);
-                accumulate(col0, hf0, pass, a);
-            }
-            if (hf0 == 1) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) half_s[r][(4 * e4 + j) & 255] = a[j];
-            }
-        }
-        __syncthreads();
-        if (active && hf0 == 0) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (4 * e4 + j < hd) write_out(r, 4 * e4 + j, (a[j] + half_s[r][4 * e4 + j]) / l_s[r]);
-        }
-    } else {
-        // one share: a thread per column, several columns a thread when there are more than NT
-        for (int col = (int)threadIdx.x; col < pairs; col += NT) {
-            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int pass = 0; pass < passes; ++pass) {
-                if (pass || col != col0) burst(col, 0, pass);
-                accumulate(col, 0, pass, a);
-            }
-            const int r = col / c4n, e4 = col - r * c4n;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (4 * e4 + j < hd) write_out(r, 4 * e4 + j, a[j] / l_s[r]);
-        }
-    }
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(part), (short)0, part_bytes,
+                                                                       0x00020000);
+    const int rec0 = (int)(((size_t)b * heads + kvh * group) * splits * (size_t)RS * 4);
+    merge_records<BF16IO, R, DEC_NW>(prs, rec0, splits * RS * 4, RS * 4, hd, group, used, wt_s, lsum_s, sh_s, out,
+                                     (size_t)b * heads + kvh * group);
 }
 
 #ifndef ATTN_NW
@@ -1098,11 +1203,11 @@ static void launch_split_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int 
 #define ATTN_DEC_BPC 1
 #endif
 
-template <int F, int LPP, bool BF16IO, int R, bool FUSE>
+template <int F, int LPP, bool BF16IO, int R, bool FUSE, int U>
 static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
     hipEvent_t t0, t1;
     g->kernel_events(t0, t1);
-    auto kern = attention_decode<F, LPP, BF16IO, R, FUSE>;
+    auto kern = attention_decode<F, LPP, BF16IO, R, FUSE, U>;
     if (t0)
         hipExtLaunchKernelGGL(kern, grid, dim3(64 * DEC_NW), 0u, g->stream, t0, t1, 0u, a.q, a.fuse, a.tables,
                               a.table_stride, a.ctx, a.geom, (int)a.heads, (int)a.kv_heads, chunk, splits, scale,
@@ -1113,31 +1218,49 @@ static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int c
                                                         a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
 }
 
-template <int F, int LPP, int R>
+template <int F, int LPP, int R, int U>
 static void launch_decode_io(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
-    if (a.fuse.qkv) launch_decode<F, LPP, false, R, true>(g, a, grid, chunk, splits, scale);
-    else if (a.bf16_io) launch_decode<F, LPP, true, R, false>(g, a, grid, chunk, splits, scale);
-    else launch_decode<F, LPP, false, R, false>(g, a, grid, chunk, splits, scale);
+    if (a.fuse.qkv) launch_decode<F, LPP, false, R, true, U>(g, a, grid, chunk, splits, scale);
+    else if (a.bf16_io) launch_decode<F, LPP, true, R, false, U>(g, a, grid, chunk, splits, scale);
+    else launch_decode<F, LPP, false, R, false, U>(g, a, grid, chunk, splits, scale);
+}
+
+// U: the smallest instantiated step count covering the chunk (2, 4, 6, 8, 10, 12 or 16, at most dec_umax); steps
+// past the chunk load its last position again and weigh nothing.
+template <int F, int LPP, int R>
+static void launch_decode_u(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
+    constexpr int UMAX = dec_umax<F, R>();
+    const int step = DEC_NW * (64 / LPP);
+    const int u = (chunk + step - 1) / step;
+    if (u > UMAX) shape("decode attention chunk (steps)", (size_t)UMAX, (size_t)u);
+    if (u <= 2) launch_decode_io<F, LPP, R, 2>(g, a, grid, chunk, splits, scale);
+    else if (u <= 4) launch_decode_io<F, LPP, R, 4>(g, a, grid, chunk, splits, scale);
+    else if (u <= 6) launch_decode_io<F, LPP, R, (UMAX < 6 ? UMAX : 6)>(g, a, grid, chunk, splits, scale);
+    else if (u <= 8) launch_decode_io<F, LPP, R, (UMAX < 8 ? UMAX : 8)>(g, a, grid, chunk, splits, scale);
+    else if (u <= 10) launch_decode_io<F, LPP, R, (UMAX < 10 ? UMAX : 10)>(g, a, grid, chunk, splits, scale);
+    else if (u <= 12) launch_decode_io<F, LPP, R, (UMAX < 12 ? UMAX : 12)>(g, a, grid, chunk, splits, scale);
+    else launch_decode_io<F, LPP, R, (UMAX < 16 ? UMAX : 16)>(g, a, grid, chunk, splits, scale);
 }
 
 template <int F>
 static void launch_decode_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
     const bool r4 = a.heads / a.kv_heads <= 4;
     switch (lanes_for(a.geom.head_dim)) {
-        case 4: r4 ? launch_decode_io<F, 4, 4>(g, a, grid, chunk, splits, scale)
-                   : launch_decode_io<F, 4, 8>(g, a, grid, chunk, splits, scale); break;
-        case 8: r4 ? launch_decode_io<F, 8, 4>(g, a, grid, chunk, splits, scale)
-                   : launch_decode_io<F, 8, 8>(g, a, grid, chunk, splits, scale); break;
-        case 16: r4 ? launch_decode_io<F, 16, 4>(g, a, grid, chunk, splits, scale)
-                    : launch_decode_io<F, 16, 8>(g, a, grid, chunk, splits, scale); break;
-        default: r4 ? launch_decode_io<F, 32, 4>(g, a, grid, chunk, splits, scale)
-                    : launch_decode_io<F, 32, 8>(g, a, grid, chunk, splits, scale); break;
+        case 4: r4 ? launch_decode_u<F, 4, 4>(g, a, grid, chunk, splits, scale)
+                   : launch_decode_u<F, 4, 8>(g, a, grid, chunk, splits, scale); break;
+        case 8: r4 ? launch_decode_u<F, 8, 4>(g, a, grid, chunk, splits, scale)
+                   : launch_decode_u<F, 8, 8>(g, a, grid, chunk, splits, scale); break;
+        case 16: r4 ? launch_decode_u<F, 16, 4>(g, a, grid, chunk, splits, scale)
+                    : launch_decode_u<F, 16, 8>(g, a, grid, chunk, splits, scale); break;
+        default: r4 ? launch_decode_u<F, 32, 4>(g, a, grid, chunk, splits, scale)
+                    : launch_decode_u<F, 32, 8>(g, a, grid, chunk, splits, scale); break;
     }
 }
 
-// The one-token kernel's chunking for a context bound: about ATTN_DEC_BPC workgroups per compute unit, chunks a
-// multiple of one workgroup step and at most what one burst of loads covers; 0 when that needs more chunks than one
-// merge takes.
+// The one-token kernel's chunking for a context bound: about ATTN_DEC_BPC workgroups per compute unit in all (a
+// few workgroups past a whole number per unit would share units with others and set the launch's tail), chunks of
+// any length up to what the largest burst of loads covers. 0 when that needs more chunks
+// than the last workgroup merges.
 static int decode_chunk(const AttentionArgs &a, int cu_count, int &splits) {
     const int hd = (int)a.geom.head_dim;
     const int step = DEC_NW * (64 / lanes_for((size_t)hd));
@@ -1145,9 +1268,8 @@ static int decode_chunk(const AttentionArgs &a, int cu_count, int &splits) {
     const int umax = a.geom.format == MARIN_KV_F32 ? (r4 ? dec_umax<MARIN_KV_F32, 4>() : dec_umax<MARIN_KV_F32, 8>())
                                                    : (r4 ? dec_umax<MARIN_KV_F16, 4>() : dec_umax<MARIN_KV_F16, 8>());
     const size_t units = std::max<size_t>(a.kv_heads * a.batch, 1);
-    const size_t target = std::max<size_t>(1, ((size_t)ATTN_DEC_BPC * std::max(cu_count, 1) + units - 1) / units);
-    size_t chunk = (a.max_ctx + target - 1) / target;
-    chunk = (chunk + step - 1) / step * step;
+    const size_t per_unit = std::max<size_t>(1, (size_t)ATTN_DEC_BPC * std::max(cu_count, 1) / units);
+    size_t chunk = (a.max_ctx + per_unit - 1) / per_unit;
     chunk = std::min<size_t>(std::max<size_t>(chunk, (size_t)step), (size_t)umax * step);
     const size_t n = (a.max_ctx + chunk - 1) / chunk;
     if (n > (size_t)DEC_MAX_SPLITS) return 0;
@@ -1157,9 +1279,7 @@ static int decode_chunk(const AttentionArgs &a, int cu_count, int &splits) {
 
 static bool decode_kernel_fits(const AttentionArgs &a) {
     const size_t hd = a.geom.head_dim, group = a.heads / a.kv_heads;
-    // the (row, partial) pairs of the workgroup's reduction take a thread each
-    const size_t partials = (size_t)DEC_NW * (64 / lanes_for(hd));
-    return a.tokens == 1 && hd % 8 == 0 && hd >= 8 && group <= 8 && partials * group <= 64 * DEC_NW;
+    return a.tokens == 1 && hd % 8 == 0 && hd >= 8 && group <= 8;
 }
 
 void launch_attention(marin_gpu *g, const AttentionArgs &a) {
@@ -1183,28 +1303,32 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     int dsplits = 0;
     const int dchunk = decode_kernel_fits(a) ? decode_chunk(a, g->cu_count, dsplits) : 0;
     if (dchunk) {
+        if (a.fuse.qkv && !a.fuse.rope) unsupported("fused decode attention without a RoPE table", 1, 0);
         if (a.batch * a.kv_heads > a.counter_count) shape("attention chunk counters", a.batch * a.kv_heads, a.counter_count);
         const size_t dneed = a.batch * a.heads * (size_t)dsplits * (size_t)rec_floats((int)a.geom.head_dim);
         if (dsplits > 1 && dneed > a.partial_floats) shape("attention partial records (floats)", dneed, a.partial_floats);
         if (a.partial_floats * 4 >= ((size_t)1 << 31))
             unsupported("attention partial bytes", (size_t)1 << 31, a.partial_floats * 4);
-        if (g->only && strcmp(g->only, "attention_decode")) return;
-        dim3 dgrid((unsigned)dsplits, (unsigned)a.kv_heads, (unsigned)a.batch);
-        switch (a.geom.format) {
-            case MARIN_KV_F32: launch_decode_f<MARIN_KV_F32>(g, a, dgrid, dchunk, dsplits, scale); break;
-            case MARIN_KV_F16: launch_decode_f<MARIN_KV_F16>(g, a, dgrid, dchunk, dsplits, scale); break;
-            default: launch_decode_f<MARIN_KV_BF16>(g, a, dgrid, dchunk, dsplits, scale); break;
+        if (!(g->only && strcmp(g->only, "attention_decode"))) {
+            dim3 dgrid((unsigned)dsplits, (unsigned)a.kv_heads, (unsigned)a.batch);
+            switch (a.geom.format) {
+                case MARIN_KV_F32: launch_decode_f<MARIN_KV_F32>(g, a, dgrid, dchunk, dsplits, scale); break;
+                case MARIN_KV_F16: launch_decode_f<MARIN_KV_F16>(g, a, dgrid, dchunk, dsplits, scale); break;
+                default: launch_decode_f<MARIN_KV_BF16>(g, a, dgrid, dchunk, dsplits, scale); break;
+            }
+            g->launched(marin_gpu::ATTENTION, a.bytes_hint, "attention_decode");
         }
-        g->launched(marin_gpu::ATTENTION, a.bytes_hint, "attention_decode");
-        if (dsplits > 1 && !(g->only && strcmp(g->only, "attention_decode_merge"))) {
+        if (ATTN_MERGE_KERNEL && dsplits > 1 && !(g->only && strcmp(g->only, "attention_decode_merge"))) {
             dim3 mgrid((unsigned)a.kv_heads, (unsigned)a.batch);
             const bool r4 = a.heads / a.kv_heads <= 4;
+            const int pb = (int)(a.partial_floats * 4);
+            const int hd = (int)a.geom.head_dim, H = (int)a.heads, KV = (int)a.kv_heads;
             if (a.bf16_io) {
-                if (r4) attention_decode_merge<true, 4><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
-                else attention_decode_merge<true, 8><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
+                if (r4) attention_decode_merge<true, 4><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
+                else attention_decode_merge<true, 8><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
             } else {
-                if (r4) attention_decode_merge<false, 4><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
-                else attention_decode_merge<false, 8><<<mgrid, 256, 0, g->stream>>>(a.partials, a.ctx, (int)a.geom.head_dim, (int)a.heads, (int)a.kv_heads, dchunk, dsplits, a.out);
+                if (r4) attention_decode_merge<false, 4><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
+                else attention_decode_merge<false, 8><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
             }
             g->launched(marin_gpu::OTHER, 0.0, "attention_decode_merge");
         }
@@ -1212,7 +1336,7 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     }
     // the fused inputs of attention_split are one sequence's token rows
     if (a.fuse.qkv && a.batch > 1) unsupported("fused attention over a batch (one-token decode only)", 1, a.batch);
-    if (prefill_fa_fits(a) && !getenv("MARIN_NO_FA")) {
+    if (prefill_fa_fits(a) && g->fast_attention) {
         if (g->only && strcmp(g->only, "fa_prefill")) return;
         launch_prefill_fa(g, a);
         return;
@@ -1412,6 +1536,13 @@ void marin_kv_clear(marin_kv *kv) {
 }
 
 size_t marin_kv_len(const marin_kv *kv) { return kv->len; }
+int marin_kv_is_empty(const marin_kv *kv) { return kv->len == 0; }
+marin_kv_format marin_kv_format_of(const marin_kv *kv) { return kv->format; }
+size_t marin_kv_auxiliary_bytes(const marin_kv *kv) {
+    // the split-attention scratch (partial records and chunk counters), the device page table and the context word
+    return kv->partial_floats * 4 + attention_counters(1, 8, kv->heads) * 4 + std::max<size_t>(kv->pool.limit, 1) * 8 +
+           4;
+}
 size_t marin_kv_capacity(const marin_kv *kv) { return kv->capacity; }
 size_t marin_kv_pages_in_use(const marin_kv *kv) { return kv->table.ids.size(); }
 size_t marin_kv_page_bytes(const marin_kv *kv) { return kv->page_bytes(); }

@@ -65,6 +65,7 @@ size_t kv_elem_bytes(marin_kv_format f);
 struct AttnFuse {
     const float *qkv = nullptr;
     const float *q_norm = nullptr, *k_norm = nullptr, *freq = nullptr;
+    const float2 *rope = nullptr;  // cos/sin of every position, [pos][hd/2] (required by the one-token kernel)
     float eps = 0.0f;
 };
 

@@ -151,6 +151,7 @@ struct marin_qwen3_cache {
     float *attn_partials = nullptr;
     size_t attn_partial_floats = 0;
     uint32_t *attn_counters = nullptr;
+    float2 *rope = nullptr;  // RoPE cos/sin of every position of the capacity
     hipGraphExec_t graph = nullptr;
     size_t graph_capacity_ctx = 0;
 };
@@ -281,12 +282,13 @@ struct PassIo {
     size_t partial_floats;
     uint32_t *counters;
     size_t counter_count;
+    const float2 *rope;
 };
 
 static PassIo io_of(marin_qwen3_cache *c, size_t n) {
     return PassIo{c->hidden, c->qkv, c->ctx, c->act, c->logits, c->best, c->kv->page_ptrs, 0, c->state + 1, 1, n,
                   c->kv, c->attn_partials, c->attn_partial_floats, c->attn_counters,
-                  attention_counters(1, CHUNK, c->model->cfg.heads)};
+                  attention_counters(1, CHUNK, c->model->cfg.heads), c->rope};
 }
 
 // One pass at the positions in the device state, whose embeddings are already in io.hidden. With one sequence,
@@ -319,6 +321,7 @@ static void pass(marin_qwen3 *m, const PassIo &io, size_t max_ctx, size_t host_c
         a.fuse.q_norm = L.q_norm;
         a.fuse.k_norm = L.k_norm;
         a.fuse.freq = m->freq;
+        a.fuse.rope = io.rope;
         a.fuse.eps = cfg.rms_eps;
         a.tables = io.tables;
         a.table_stride = io.table_stride;
@@ -505,6 +508,7 @@ marin_status marin_qwen3_cache_new(marin_qwen3 *m, size_t capacity, marin_kv_for
             c->attn_partial_floats = attention_partial_floats(1, CHUNK, cfg.heads, cfg.head_dim, capacity, g->cu_count);
             c->attn_partials = (float *)g->alloc(c->attn_partial_floats * 4, false);
             c->attn_counters = (uint32_t *)g->alloc(attention_counters(1, CHUNK, cfg.heads) * 4, true);
+            c->rope = make_rope_table(g, m->freq, cfg.head_dim, capacity);
         } catch (...) {
             marin_qwen3_cache_free(c.release());
             throw;
@@ -521,7 +525,7 @@ void marin_qwen3_cache_free(marin_qwen3_cache *c) {
     marin_kv_free(c->kv);
     for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->logits, (void *)c->ctx, (void *)c->act,
                     (void *)c->best, (void *)c->ids, (void *)c->state, (void *)c->attn_partials, (void *)c->attn_counters,
-                    (void *)c->tokens_out})
+                    (void *)c->tokens_out, (void *)c->rope})
         g->release(p);
     delete c;
 }
@@ -753,7 +757,7 @@ static void free_batch_graph(marin_qwen3_batch *b) {
 static PassIo io_of(marin_qwen3_batch *b) {
     return PassIo{b->hidden, b->qkv, b->ctx, b->act, b->logits, b->best, b->tables, b->table_stride,
                   b->state + b->seqs.size(), b->seqs.size(), 1, b->seqs[0]->kv, b->partials, b->partial_floats,
-                  b->counters, b->counter_count};
+                  b->counters, b->counter_count, b->seqs[0]->rope};
 }
 
 // One batch decode step: every sequence's choice becomes its token, then one pass of the batch.

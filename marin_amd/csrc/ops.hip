@@ -75,6 +75,26 @@ float *make_rope_frequencies(marin_gpu *g, size_t hd, float theta) {
     return d;
 }
 
+// Cosine and sine of the RoPE angle pos * freq[i] for positions 0 .. positions - 1, [pos][hd/2] (the same sincosf
+// of the same f32 angle that rope_kernel computes, so a table lookup gives the same bits).
+__global__ void rope_table_kernel(const float *__restrict__ freq, int half, size_t positions, float2 *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= positions * half) return;
+    const float position = (float)(i / half);
+    float s, c;
+    sincosf(position * freq[i % half], &s, &c);
+    out[i] = make_float2(c, s);
+}
+
+float2 *make_rope_table(marin_gpu *g, const float *freq, size_t hd, size_t positions) {
+    const size_t n = std::max<size_t>(positions, 1) * std::max<size_t>(hd / 2, 1);
+    float2 *t = (float2 *)g->alloc(n * sizeof(float2), false);
+    rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, g->stream>>>(freq, (int)(hd / 2),
+                                                                           std::max<size_t>(positions, 1), t);
+    g->launched();
+    return t;
+}
+
 void forget_rope_frequencies(marin_gpu *g) {
     std::lock_guard<std::mutex> lock(g_freq_mutex);
     for (auto it = g_freq.begin(); it != g_freq.end();) {

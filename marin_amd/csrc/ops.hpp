@@ -12,5 +12,7 @@ const float *rope_frequencies(marin_gpu *g, size_t hd, float theta);
 void forget_rope_frequencies(marin_gpu *g);
 // The same table in memory the caller owns (released with gpu->release).
 float *make_rope_frequencies(marin_gpu *g, size_t hd, float theta);
+// RoPE cos/sin table [positions][hd/2] (float2) from a frequency table, on the device.
+float2 *make_rope_table(marin_gpu *g, const float *freq, size_t hd, size_t positions);
 
 }  // namespace marin
