@@ -167,6 +167,15 @@ marin_status marin_matmul_triple(marin_gpu *gpu, const marin_matrix *w0, const m
                                  const marin_matrix *w2, const marin_buffer *x, size_t tokens, marin_buffer *y0,
                                  marin_buffer *y1, marin_buffer *y2);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc): marin_matmul_quant_bf16 with the multi-token products' scratch
+ * (activation limbs, exponents, per-token factors) in a fixed 4 MiB device array of the library, one per device for
+ * the life of the process, instead of memory the library allocates. Calls no allocating routine. Refuses (Unsupported)
+ * a product whose scratch would exceed 4 MiB (about 64 tokens of 12288 columns). Every call on a device shares the
+ * array: calls that overlap on one device (contexts whose streams run at once) race. */
+marin_status marin_matmul_quant_bf16_noalloc(marin_gpu *gpu, const marin_quant_matrix *w, const marin_buffer *x,
+                                             size_t tokens, marin_buffer *out);
+
 /* ---- elementwise ops: crates/cuda/src/ops.rs:110-236 ---- */
 marin_status marin_rms_norm(marin_gpu *gpu, marin_buffer *x, const marin_buffer *weight, float eps); /* ops.rs:110 */
 marin_status marin_rms_norm_into(marin_gpu *gpu, const marin_buffer *x, const marin_buffer *weight,

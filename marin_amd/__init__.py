@@ -423,6 +423,11 @@ class Gpu:
     def matmul_quant_bf16(self, w: DeviceQuantMatrix, x: Buffer, tokens: int, out: Buffer) -> None:
         check(lib.marin_matmul_quant_bf16(self._h, w._h, x.handle, tokens, out.handle))
 
+    def matmul_quant_bf16_noalloc(self, w: DeviceQuantMatrix, x: Buffer, tokens: int, out: Buffer) -> None:
+        """matmul_quant_bf16 with its scratch in the library's fixed device array (no allocation; see
+        include/marin_hip.h)."""
+        check(lib.marin_matmul_quant_bf16_noalloc(self._h, w._h, x.handle, tokens, out.handle))
+
     # ---- elementwise (ops.rs) ----
     def rms_norm(self, x: Buffer, weight: Buffer, eps: float) -> None:
         check(lib.marin_rms_norm(self._h, x.handle, weight.handle, eps))

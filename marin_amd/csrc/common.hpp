@@ -133,6 +133,10 @@ struct marin_gpu {
     void *work = nullptr;
     size_t work_bytes = 0;
     void *workspace(size_t bytes);
+    // While set, workspace() hands out this caller-owned device memory instead (and refuses a larger request with
+    // Unsupported), so a call allocates nothing (the allocation-free entry points).
+    void *fixed_work = nullptr;
+    size_t fixed_work_bytes = 0;
     // Device fault word: kernels that meet input the reference rejects (non-finite router logits) set a bit and
     // carry on with harmless values; the next blocking call (synchronize, download) reports it and clears it.
     uint32_t *fault = nullptr;

@@ -89,6 +89,10 @@ void marin_gpu::release(void *p) {
 }
 
 void *marin_gpu::workspace(size_t bytes) {
+    if (fixed_work) {
+        if (bytes > fixed_work_bytes) unsupported("scratch bytes of an allocation-free call", fixed_work_bytes, bytes);
+        return fixed_work;
+    }
     if (bytes <= work_bytes) return work;
     HIP_CHECK(hipStreamSynchronize(stream));
     if (work) (void)hipFree(work);
