@@ -15,8 +15,8 @@ stream they run on, which gives its mean launch duration (kernel time plus the g
 dominant kernel is the product instantiation with the most time per step; `achieved` is its algorithmic bytes per
 launch over its mean launch duration (`kernels` lists every instantiation the same way). `traffic` is that kernel's HBM bytes per launch
 from the committed rocprofv3 counter runs (profiles/traffic.json), when present. `cpu_baseline`
-times the CPU oracle (oracle/marin_oracle.c, a C restatement of Marin's single-threaded int8 decode GEMV and
-attention) on one core over a bounded sample of the same token's work.
+times one real decode token of the CPU oracle (oracle/marin_oracle.c, a C restatement of Marin's single-threaded int8
+decode) on one core with the same cache format and context, and states the host's core count.
 """
 from __future__ import annotations
 
@@ -38,51 +38,65 @@ def layer_params(shape: dict) -> int:
     return shape["layers"] * (H * (qd + 2 * kvd) + qd * H + 3 * F * H)
 
 
-def cpu_baseline(shape: dict, ctx: int, budget_s: float = 12.0) -> dict:
-    """Seconds per 8B decode token on one host core: every projection shape of one layer (x36), the output head,
-    and attention over `ctx` f32 cached positions for every layer, with the oracle's Q8Gemv and AttendOne."""
+def cpu_baseline(shape: dict, ctx: int, kv_f16: bool) -> dict:
+    """One real decode token on the host: the CPU oracle's Qwen3 forward (oracle/marin_oracle.c, a C restatement of
+    Marin's int8 decode: Q8Gemv products, AttendOne attention) through every layer and the output head after `ctx`
+    cached positions in the GPU line's KV format, on one thread, as Marin decodes one token
+    (crates/tensor/src/q8.rs:67-74). Weight values do not change the time, so the model is a constant code pattern
+    and a filled cache rather than generated weights and a CPU prompt pass."""
+    import ctypes as C
+
     from oracle import oracle as o
-    o.set_threads(1)
-    rng = np.random.default_rng(0)
-    H, F, V, L = shape["hidden"], shape["ffn"], shape["vocab"], shape["layers"]
-    qd, kvd, g = shape["heads"] * shape["head_dim"], shape["kv_heads"] * shape["head_dim"], shape["group"]
-    mats = [(qd, H), (kvd, H), (kvd, H), (H, qd), (F, H), (F, H), (H, F)]
-
-    def gemv_time(rows, cols, reps=1):
-        codes = rng.integers(0, 256, rows * cols, dtype=np.uint8)
-        codes[codes == 128] = 127
-        scales = rng.random(rows * cols // g, dtype=np.float32) * np.float32(1e-3)
-        x = rng.standard_normal(cols).astype(np.float32)
-        out = np.zeros(rows, np.float32)
-        t = time.perf_counter()
-        for _ in range(reps):
-            o.lib.or_q8_gemv(codes.ctypes.data, scales.ctypes.data, x.ctypes.data, out.ctypes.data, rows, cols, g)
-        return (time.perf_counter() - t) / reps
-
-    t0 = time.perf_counter()
-    layer = sum(gemv_time(r, c) for r, c in mats)
-    head = gemv_time(V, H)
-    hd = shape["head_dim"]
-    q = rng.standard_normal(qd).astype(np.float32)
-    kv = rng.standard_normal(2 * ctx * kvd).astype(np.float32)
-    out = np.zeros(qd, np.float32)
+    lib = o.lib
+    lib.or_qwen3_time_token.restype = C.c_double
+    lib.or_qwen3_time_token.argtypes = [C.c_void_p, C.c_size_t]
+    cfg = o._SynthConfig(layers=shape["layers"], hidden=shape["hidden"], heads=shape["heads"],
+                         kv_heads=shape["kv_heads"], head_dim=shape["head_dim"], ffn=shape["ffn"],
+                         vocab=shape["vocab"], group=shape["group"], capacity=0, eps=shape["eps"],
+                         theta=shape["theta"], tied=int(shape["tied"]), kv_f16=int(kv_f16), seed=1)
     t = time.perf_counter()
-    o.lib.or_attention(q.ctypes.data, kv.ctypes.data, kv.ctypes.data + ctx * kvd * 4, out.ctypes.data,
-                       shape["heads"], shape["kv_heads"], hd, ctx - 1, 1)
-    attn = time.perf_counter() - t
-    per_token = L * (layer + attn) + head
-    reps = 1
-    while time.perf_counter() - t0 < budget_s and reps < 4:  # a second pass steadies the estimate
-        layer2 = sum(gemv_time(r, c) for r, c in mats)
-        per_token = min(per_token, L * (layer2 + attn) + head)
-        reps += 1
-    return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"one {L}-layer token: each projection shape of one layer x{L}, output head once, attention "
-                      f"over {ctx} f32 positions x{L}; oracle Q8Gemv/AttendOne on 1 core, best of {reps}",
-            "seconds_per_token": round(per_token, 4)}
+    sec = lib.or_qwen3_time_token(C.byref(cfg), ctx)
+    wall = time.perf_counter() - t
+    if sec <= 0:
+        return {"value": None, "unit": "tok/s", "cores": 1, "kind": "port",
+                "sample": f"oracle token failed ({sec})", "host_cores": os.cpu_count()}
+    return {"value": round(1.0 / sec, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"one real {shape['layers']}-layer decode token after {ctx} cached positions "
+                      f"({'f16' if kv_f16 else 'f32'} cache), oracle or_qwen3_forward on 1 thread "
+                      f"({wall:.1f}s with setup)",
+            "seconds_per_token": round(sec, 4), "host_cores": os.cpu_count()}
 
 
-MOE = {"layers": 48, "hidden": 2048, "experts": 128, "ffn": 768, "k": 8, "group": 128}
+MOE = {"layers": 48, "hidden": 2048, "experts": 128, "ffn": 768, "k": 8, "group": 128, "heads": 32, "kv_heads": 4,
+       "head_dim": 128, "context": 2048}
+
+
+def moe_attention_us(m, gpu, c, batch, rng, reps) -> float:
+    """Per-layer decode attention of the MoE stack: `batch` sequences at `context` positions each, 32 q / 4 kv heads,
+    head_dim 128, bf16 pages of 16 positions; one pool per layer (every layer's keys and values distinct, 48 layers
+    streamed in turn). Mean microseconds per layer over `reps` passes of the 48 layers."""
+    L, kvh, hd, heads, ctx, pt = c["layers"], c["kv_heads"], c["head_dim"], c["heads"], c["context"], 16
+    per_seq = -(-ctx // pt)
+    block = _bf16(rng.standard_normal((64, 2 * pt * kvh * hd)))
+    tables = np.arange(batch * per_seq, dtype=np.uint32).reshape(batch, per_seq)
+    ctxs = np.full(batch, ctx, np.uint32)
+    pools = []
+    for l in range(L):
+        pool = m.PagePool(gpu, batch * per_seq, pt, kvh, hd, m.KvFormat.BF16)
+        for pid in range(batch * per_seq):
+            pool.write_page(pid, block[(pid + l) % 64])
+        pools.append(pool)
+    q = gpu.typed(m.Dtype.BF16, host=_bf16(rng.standard_normal((batch, heads, hd))))
+    out = gpu.typed(m.Dtype.BF16, batch * heads * hd)
+    for pool in pools:
+        pool.attention(q, tables, ctxs, heads, out)
+    gpu.synchronize()
+    a = gpu.mark()
+    for _ in range(reps):
+        for pool in pools:
+            pool.attention(q, tables, ctxs, heads, out)
+    b = gpu.mark()
+    return b.since(a) / (reps * L) * 1e6
 
 
 def bench_moe(m, args) -> int:
@@ -138,6 +152,11 @@ def bench_moe(m, args) -> int:
                           "down_us_per_layer": round(parts[1] * 1e6 / L, 2),
                           "gate_up_GBps": round(union * 2 * F * H * (1 + 4 / G) / parts[0] / 1e9, 1),
                           "down_GBps": round(union * F * H * (1 + 4 / G) / parts[1] / 1e9, 1)}
+        att_us = moe_attention_us(m, gpu, c, batch, rng, reps)
+        results[batch]["attention_us_per_layer"] = round(att_us, 2)
+        results[batch]["layer_us"] = round(sec * 1e6 / L + att_us, 2)
+        print(f"[bench] moe batch {batch}: attention at ctx {c['context']}: {att_us:.1f} us/layer", file=sys.stderr,
+              flush=True)
         print(f"[bench] moe batch {batch}: {sec * 1e6:.1f} us per {L}-layer stack, {union / L:.1f} experts/layer, "
               f"{algo / sec / 1e9:.0f} GB/s (gate_up {parts[0] * 1e6 / L:.1f} us/layer, down "
               f"{parts[1] * 1e6 / L:.1f} us/layer)", file=sys.stderr, flush=True)
@@ -150,7 +169,8 @@ def bench_moe(m, args) -> int:
         "data": "synthetic (random-init N(0,0.02) experts quantized int8 g128 on device; N(0,1) hidden states; "
                 "random-init router weights)",
         "config": {"workload": "qwen3-30b-a3b expert FFN stack (48 layers, 128 experts x ffn 768, top-8, hidden "
-                               "2048), batch 1; batch 8 under batches", **c},
+                               "2048), batch 1; batch 8 under batches; each layer's decode attention at 2048 "
+                               "positions (32 q / 4 kv heads) timed beside it (attention_us_per_layer)", **c},
         "roofline": {"bound": "hbm", "kernel": "gemv_decode (tile-mapped) + expert_down", "achieved": r1["GBps"],
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(r1["GBps"] / HBM_PEAK_GBPS, 4),
                      "traffic": None},
@@ -278,7 +298,11 @@ def bench_paged(m, args) -> int:
     pages_each = [-(-int(c) // pt) for c in ctx]
     total = sum(pages_each)
     perm = rng.permutation(total)
-    pool = m.PagePool(gpu, total, pt, kvh, hd, m.KvFormat.BF16)
+    # copies of the pool totalling at least twice the 256 MB last-level cache, used in turn, so every call streams its
+    # keys and values from HBM
+    page_bytes = 2 * pt * kvh * hd * 2
+    npools = max(2, -(-(2 * 256 << 20) // (total * page_bytes)))
+    pools = [m.PagePool(gpu, total, pt, kvh, hd, m.KvFormat.BF16) for _ in range(npools)]
     stride = max(pages_each)
     tables = np.zeros((batch, stride), np.uint32)
     block = _bf16(rng.standard_normal((64, 2 * pt * kvh * hd)))  # 64 distinct pages of random rows, dealt cyclically
@@ -287,17 +311,18 @@ def bench_paged(m, args) -> int:
         for i in range(pages_each[b]):
             pid = int(perm[at])
             tables[b, i] = pid
-            pool.write_page(pid, block[at % 64])
+            for pool in pools:
+                pool.write_page(pid, block[at % 64])
             at += 1
     q = gpu.typed(m.Dtype.BF16, host=_bf16(rng.standard_normal((batch, heads, hd))))
     out = gpu.typed(m.Dtype.BF16, batch * heads * hd)
-    for _ in range(5):
-        pool.attention(q, tables, ctx, heads, out)
+    for i in range(2 * npools):
+        pools[i % npools].attention(q, tables, ctx, heads, out)
     gpu.synchronize()
-    steps = max(args.steps, 20)
+    steps = max(args.steps, 20) // npools * npools
     a = gpu.mark()
-    for _ in range(steps):
-        pool.attention(q, tables, ctx, heads, out)
+    for i in range(steps):
+        pools[i % npools].attention(q, tables, ctx, heads, out)
     b = gpu.mark()
     sec = b.since(a) / steps
     nbytes = int(ctx.sum()) * kvh * hd * 2 * 2 + 2 * batch * heads * hd * 2
@@ -308,7 +333,8 @@ def bench_paged(m, args) -> int:
         "metric": "batched paged GQA decode attention HBM GB/s (batch 16, ragged contexts)", "value": round(gbps, 1),
         "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": 5, "ms_per_step": round(sec * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (bf16 N(0,1) q/k/v; 64 distinct random pages dealt over the pool)",
+        "data": f"synthetic (bf16 N(0,1) q/k/v; 64 distinct random pages dealt over the pool; {npools} copies of the "
+                f"pool ({npools * total * page_bytes / 1e6:.0f} MB) used in turn)",
         "config": {"workload": "config 2: batch 16, 32 q / 8 kv heads, head_dim 128, 16-position pages, contexts "
                                "uniform in [512, 8192], shuffled page tables from one pool", "contexts": ctx.tolist()},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -479,7 +505,7 @@ def main() -> int:
         "first_tokens": tokens[:8].tolist(),
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(shape, args.prompt)
+        line["cpu_baseline"] = cpu_baseline(shape, args.prompt, args.kv == "f16")
     print(json.dumps(line), flush=True)
     return 0
 

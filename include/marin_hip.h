@@ -275,6 +275,11 @@ marin_status marin_qwen3_cache_truncate(marin_qwen3_cache *c, size_t len);
  * (vocab floats, host memory). */
 marin_status marin_qwen3_forward(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n,
                                  float *logits);
+/* CausalLm::forward_rows (runtime/src/lib.rs:86-99; Qwen3Gpu::forward_rows, model/src/qwen3/gpu.rs:212-236): one pass
+ * over n <= 8 tokens (more: Unsupported, nothing run) that commits them and writes the logits after every token,
+ * [n][vocab] floats in host memory; a decode that follows continues from the last row's greedy choice. */
+marin_status marin_qwen3_forward_rows(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n,
+                                      float *logits);
 /* runtime::generate_reusing greedy (generate.rs:105-284, sampler lowest-index argmax): the prompt, then `steps`
  * greedy tokens chosen on the device; no host round trip per token. */
 marin_status marin_qwen3_generate(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *prompt, size_t n,

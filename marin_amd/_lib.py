@@ -62,6 +62,7 @@ SIGNATURES = {
     "marin_matmul_pair": (st, [P, P, P, P, sz, P, P]),
     "marin_matmul_triple": (st, [P, P, P, P, P, sz, P, P, P]),
     "marin_matmul_quant_bf16_noalloc": (st, [P, P, P, sz, P]),
+    "marin_qwen3_forward_rows": (st, [P, P, P, sz, P]),
     "marin_kv_is_empty": (C.c_int, [P]),
     "marin_kv_format_of": (C.c_int, [P]),
     "marin_kv_auxiliary_bytes": (sz, [P]),

@@ -33,16 +33,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BW = 8;      // waves per block
 // items in flight per wave: 8 for one token tile; 4 for two, so two blocks stay resident per compute unit
-#ifndef BATCH_RING2
-#define BATCH_RING2 4
-#endif
-#ifndef BATCH_BRES
-#define BATCH_BRES 1
-#endif
+constexpr int BATCH_RING2 = 4;
 // 8-window slices keep the wave's B fragments (all its windows, every token tile) in registers for the whole launch,
 // so only the codes stream; the registers leave one block per compute unit, and the ring is one slice deep
 template <int SM>
-constexpr bool bres() { return BATCH_BRES && SM == 8; }
+constexpr bool bres() { return SM == 8; }
 template <int TT, int SM>
 constexpr int bring() { return bres<SM>() ? SM : (TT == 1 ? 8 : BATCH_RING2); }
 template <int SM>

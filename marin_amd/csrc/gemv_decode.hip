@@ -30,21 +30,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-#ifndef DECODE_RING
-#define DECODE_RING 8
-#endif
-constexpr int RING = DECODE_RING;  // code windows in flight per wave
-#ifndef DECODE_BPC
-#define DECODE_BPC 2
-#endif
-constexpr int DECODE_BLOCKS_PER_CU = DECODE_BPC;
-#ifndef DECODE_BRES
-#define DECODE_BRES 1
-#endif
-#ifndef DECODE_HALF
-#define DECODE_HALF 1
-#endif
-constexpr int MAP_MAX = 64;  // tile map entries (selected experts) a launch may carry: one per lane  // resident blocks the persistent grid aims at per compute unit
+constexpr int RING = 8;                  // code windows in flight per wave
+constexpr int DECODE_BLOCKS_PER_CU = 2;  // resident blocks the persistent grid aims at per compute unit
+constexpr int MAP_MAX = 64;              // tile map entries (selected experts) a launch may carry: one per lane
 
 // Lane permutations inside rows of 16 lanes (DPP): 0xB1 swaps neighbours, 0x4E swaps pairs, 0x141 mirrors each
 // half row of 8 lanes.
@@ -77,15 +65,6 @@ __device__ __forceinline__ floatx4 scales4(const ST *p) {
 
 }  // namespace
 
-// Timeline stamps for tuning (built only with -DDECODE_TRACE): per block, the 100 MHz wall clock at entry (0),
-// activation loads issued (1), ring issued (2), limbs built (4), after the prologue barrier (5), first tile done (6)
-// and exit (7).
-#ifdef DECODE_TRACE
-__device__ unsigned long long decode_trace[4096 * 8];
-#define TRACE(k) do { if (threadIdx.x == 0 && blockIdx.x < 4096) decode_trace[blockIdx.x * 8 + (k)] = wall_clock64(); } while (0)
-#else
-#define TRACE(k) do { } while (0)
-#endif
 
 // BITS 8 or 4; WG = 64-column windows per quantization group (group = 64 * WG); SM = windows per wave per tile
 // (wave w owns windows [w * SM, (w + 1) * SM) of every row; waves past the last window hold no groups); ST = scale
@@ -100,7 +79,6 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
                                                        GemvIn in, GemvOut out, int rows, int cols, int tiles,
                                                        int half) {
     extern __shared__ __align__(16) unsigned char lds[];
-    TRACE(0);
     constexpr int S = SM;
     constexpr int CB = BITS == 8 ? 16 : 8;  // code bytes per lane per window
     const int lane = threadIdx.x & 63;
@@ -154,7 +132,6 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         }
     }
 
-    TRACE(1);
     // ---- the ring: item i = (tile blockIdx + (i / S) * grid, window w0 + i % S)
     typedef typename std::conditional<BITS == 8, u32x4, u32x2>::type Raw;
     Raw ring[RING];
@@ -192,7 +169,6 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     for (int j = 0; j < RING; ++j) load_item(min(j, last), j);
     const int t_last = tile_of((int)blockIdx.x + (last / S) * (int)gridDim.x);  // refills past the last item
     const int w_last = min(w0 + last % S, windows - 1);
-    TRACE(2);
 
     // ---- prologue: the limbs (and the RMSNorm partial sums: the threads' columns cover the row once)
     float xv[R][16];
@@ -292,9 +268,7 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             }
         }
     }
-    TRACE(4);
     __syncthreads();
-    TRACE(5);
     float rs = 1.0f;
     if (norm) {
         float total = 0.0f;
@@ -303,8 +277,8 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         rs = 1.0f / sqrtf(total / (float)cols + in.eps);
     }
 
-    // DECODE_BRES: slices one ring round long keep their B fragments in registers for the launch
-    constexpr bool BRES = DECODE_BRES && S == RING;
+    // slices one ring round long keep their B fragments in registers for the launch
+    constexpr bool BRES = S == RING;
     int4v bq[BRES ? S : 1];
     if constexpr (BRES) {
 #pragma unroll
@@ -393,7 +367,6 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
                 if (c == 0) *reinterpret_cast<float4 *>(rb + wave * 16 + 4 * q) = make_float4(r4[0], r4[1], r4[2], r4[3]);
                 total = (floatx4){0.f, 0.f, 0.f, 0.f};
                 __syncthreads();
-                if (tile_n == 0) TRACE(6);
                 if (wave == 0 && lane < 16) {
                     float v = 0.0f;
 #pragma unroll
@@ -429,7 +402,6 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             }
         }
     }
-    TRACE(7);
     if (out.argmax && wave == 0) {
         for (int o = 8; o > 0; o >>= 1) {
             const unsigned long long other = __shfl_xor(best, o);
@@ -484,7 +456,7 @@ static const char *launch_decode_t(marin_gpu *g, const marin_quant_matrix *w, co
     // more: 384 tiles on 256 units put 2 tiles on half of them, 768 half tiles put 3 halves on each. A half tile
     // costs a whole tile's instructions for half its bytes, so nowhere else.
     const int full_load = (tiles + cu - 1) / cu, half_load2 = (2 * tiles + cu - 1) / cu;  // (half tiles: x 2)
-    const int half = DECODE_HALF && !in.tile_map && 5 * half_load2 <= 8 * full_load ? 1 : 0;
+    const int half = !in.tile_map && 5 * half_load2 <= 8 * full_load ? 1 : 0;
     const int items = tiles << half;
     const int blocks = std::min(items, std::min(resident, DECODE_BLOCKS_PER_CU) * cu);
     if (g->only && name != g->only) {
@@ -527,11 +499,6 @@ bool gemv_decode_supported(const marin_quant_matrix *w) {
     return gemv_supported(w) && (w->group == 64 || w->group == 128) && slice_windows((int)(w->cols / 64), dw) > 0;
 }
 
-#ifdef DECODE_TRACE
-extern "C" void marin_decode_trace_read(unsigned long long *host) {
-    (void)hipMemcpyFromSymbol(host, HIP_SYMBOL(decode_trace), sizeof(decode_trace));
-}
-#endif
 
 const char *launch_gemv_decode(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out) {
     if (w->bf16_scales) return launch_decode_st<uint16_t>(g, w, in, out);

@@ -29,10 +29,8 @@ using namespace marin;
 
 namespace marin {
 
-#ifndef MARIN_PREFILL_CHUNK
-#define MARIN_PREFILL_CHUNK 512
-#endif
-constexpr size_t CHUNK = MARIN_PREFILL_CHUNK;  // tokens per prompt pass through the layers (the products run as GEMMs)
+constexpr size_t MAX_ROWS = 8;  // tokens of a forward_rows pass (model/src/qwen3/gpu.rs:118-119)
+constexpr size_t CHUNK = 512;  // tokens per prompt pass through the layers (the products run as GEMMs)
 
 // One decode step's bookkeeping, after the output head left the greedy choice in *best as (total-order key, ~id)
 // (sampler/src/lib.rs:40-48: largest logit, lowest id on ties): record the token, clear the choice for the next
@@ -78,6 +76,29 @@ __global__ __launch_bounds__(512) void advance(unsigned long long *best, uint32_
     }
     __syncthreads();
     embed_row(codes, scales, id_s, cols, group, hidden);
+}
+
+// The greedy choice of one logits row (sampler/src/lib.rs:40-48: largest under f32's total order, lowest index on
+// ties), as the key the products' fused argmax leaves: (total-order key << 32) | ~index. One block.
+__global__ __launch_bounds__(1024) void argmax_row(const float *__restrict__ row, int n, unsigned long long *best) {
+    __shared__ unsigned long long part[16];
+    unsigned long long k = 0ull;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const int b = __float_as_int(row[i]);
+        const unsigned key = (unsigned)(b ^ (int)(((unsigned)(b >> 31)) >> 1)) ^ 0x80000000u;
+        const unsigned long long v = (unsigned long long)key << 32 | (unsigned long long)(0xffffffffu - (unsigned)i);
+        k = v > k ? v : k;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(k, o);
+        k = other > k ? other : k;
+    }
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w) k = part[w] > k ? part[w] : k;
+        *best = k;
+    }
 }
 
 // Sets the device state for a pass of `count` tokens at `pos` (pos, ctx = pos + count) and clears the greedy choice
@@ -152,6 +173,7 @@ struct marin_qwen3_cache {
     size_t attn_partial_floats = 0;
     uint32_t *attn_counters = nullptr;
     float2 *rope = nullptr;  // RoPE cos/sin of every position of the capacity
+    float *rows = nullptr;   // forward_rows: logits of every row of a pass, [MAX_ROWS][vocab]
     hipGraphExec_t graph = nullptr;
     size_t graph_capacity_ctx = 0;
 };
@@ -283,12 +305,13 @@ struct PassIo {
     uint32_t *counters;
     size_t counter_count;
     const float2 *rope;
+    float *rows;  // set: the head runs over every row into rows [tokens][vocab] (one sequence)
 };
 
 static PassIo io_of(marin_qwen3_cache *c, size_t n) {
     return PassIo{c->hidden, c->qkv, c->ctx, c->act, c->logits, c->best, c->kv->page_ptrs, 0, c->state + 1, 1, n,
                   c->kv, c->attn_partials, c->attn_partial_floats, c->attn_counters,
-                  attention_counters(1, CHUNK, c->model->cfg.heads), c->rope};
+                  attention_counters(1, CHUNK, c->model->cfg.heads), c->rope, nullptr};
 }
 
 // One pass at the positions in the device state, whose embeddings are already in io.hidden. With one sequence,
@@ -361,6 +384,23 @@ static void pass(marin_qwen3 *m, const PassIo &io, size_t max_ctx, size_t host_c
         launch_product(g, L.down, act_in, add_out, n);
     }
     if (!head_out) return;  // a prompt's earlier chunks need no logits
+    if (io.rows && io.batch == 1) {
+        // every row's logits (forward_rows), then the last row's greedy choice for the decode that may follow
+        GemvIn all;
+        all.mode = IN_NORM;
+        all.x = io.hidden;
+        all.x_stride = H;
+        all.norm = m->final_norm;
+        all.eps = cfg.rms_eps;
+        GemvOut rows;
+        rows.mode = OUT_F32;
+        rows.y = io.rows;
+        rows.y_stride = cfg.vocab;
+        launch_product(g, m->head(), all, rows, n);
+        argmax_row<<<1, 1024, 0, g->stream>>>(io.rows + (n - 1) * cfg.vocab, (int)cfg.vocab, io.best);
+        g->launched();
+        return;
+    }
     GemvIn last;
     last.mode = IN_NORM;
     last.x = io.batch == 1 ? io.hidden + (n - 1) * H : io.hidden;
@@ -380,7 +420,7 @@ static void pass(marin_qwen3 *m, const PassIo &io, size_t max_ctx, size_t host_c
     }
 }
 
-static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n) {
+static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n, bool all_rows = false) {
     marin_gpu *g = m->gpu;
     const size_t start = c->kv->len;
     if (n == 0) throw Error(MARIN_SHAPE, "no tokens", 1, 0);
@@ -397,7 +437,9 @@ static void run_prompt(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids
         embed_device_ids<<<dim3((unsigned)nt), dim3(256), 0, g->stream>>>(
             m->embed->codes, (const float *)m->embed->scales, c->ids, c->hidden, (int)m->cfg.hidden, (int)m->cfg.group);
         g->launched();
-        pass(m, io_of(c, nt), start + t0 + nt, 0, t0 + nt == n);
+        PassIo io = io_of(c, nt);
+        if (all_rows) io.rows = c->rows;
+        pass(m, io, start + t0 + nt, 0, t0 + nt == n);
         c->kv->len = start + t0 + nt;
     }
 }
@@ -509,6 +551,7 @@ marin_status marin_qwen3_cache_new(marin_qwen3 *m, size_t capacity, marin_kv_for
             c->attn_partials = (float *)g->alloc(c->attn_partial_floats * 4, false);
             c->attn_counters = (uint32_t *)g->alloc(attention_counters(1, CHUNK, cfg.heads) * 4, true);
             c->rope = make_rope_table(g, m->freq, cfg.head_dim, capacity);
+            c->rows = (float *)g->alloc(MAX_ROWS * cfg.vocab * 4, false);
         } catch (...) {
             marin_qwen3_cache_free(c.release());
             throw;
@@ -525,7 +568,7 @@ void marin_qwen3_cache_free(marin_qwen3_cache *c) {
     marin_kv_free(c->kv);
     for (void *p : {(void *)c->hidden, (void *)c->qkv, (void *)c->logits, (void *)c->ctx, (void *)c->act,
                     (void *)c->best, (void *)c->ids, (void *)c->state, (void *)c->attn_partials, (void *)c->attn_counters,
-                    (void *)c->tokens_out, (void *)c->rope})
+                    (void *)c->tokens_out, (void *)c->rope, (void *)c->rows})
         g->release(p);
     delete c;
 }
@@ -538,6 +581,15 @@ marin_status marin_qwen3_forward(marin_qwen3 *m, marin_qwen3_cache *c, const uin
     return guard([&] {
         run_prompt(m, c, ids, n);
         m->gpu->download(logits, c->logits, m->cfg.vocab * 4);
+    });
+}
+
+marin_status marin_qwen3_forward_rows(marin_qwen3 *m, marin_qwen3_cache *c, const uint32_t *ids, size_t n,
+                                      float *logits) {
+    return guard([&] {
+        if (n > MAX_ROWS) unsupported("forward_rows tokens", MAX_ROWS, n);
+        run_prompt(m, c, ids, n, true);
+        m->gpu->download(logits, c->rows, n * m->cfg.vocab * 4);
     });
 }
 
@@ -757,7 +809,7 @@ static void free_batch_graph(marin_qwen3_batch *b) {
 static PassIo io_of(marin_qwen3_batch *b) {
     return PassIo{b->hidden, b->qkv, b->ctx, b->act, b->logits, b->best, b->tables, b->table_stride,
                   b->state + b->seqs.size(), b->seqs.size(), 1, b->seqs[0]->kv, b->partials, b->partial_floats,
-                  b->counters, b->counter_count, b->seqs[0]->rope};
+                  b->counters, b->counter_count, b->seqs[0]->rope, nullptr};
 }
 
 // One batch decode step: every sequence's choice becomes its token, then one pass of the batch.

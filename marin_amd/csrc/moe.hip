@@ -154,9 +154,6 @@ __global__ __launch_bounds__(64) void moe_plan(const int32_t *__restrict__ ids, 
 
 // grid: (H / 16 output tiles, tokens); a wave per expert slot j < k. WG: 64-column windows per group; MW: windows of
 // an expert's input (F / 64, at most 16) rounded up to what the template holds.
-#ifndef MOE_DOWN_HALF
-#define MOE_DOWN_HALF 1
-#endif
 
 template <int WG, int MW, typename ST>
 __global__ __launch_bounds__(64 * MOE_MAX_K) void expert_down(const uint8_t *__restrict__ codes,
@@ -286,7 +283,7 @@ template <int WG, int MW, typename ST>
 static void launch_down_t(marin_gpu *g, const marin_quant_matrix *down, const float *act, const int32_t *ids,
                           const float *weights, size_t tokens, size_t k, size_t hidden, size_t ffn, float *out) {
     // half tiles while whole tiles leave compute units idle (one token: hidden / 16 workgroups)
-    const int half = MOE_DOWN_HALF && (hidden / 16) * tokens < (size_t)std::max(g->cu_count, 1) ? 1 : 0;
+    const int half = (hidden / 16) * tokens < (size_t)std::max(g->cu_count, 1) ? 1 : 0;
     dim3 grid((unsigned)((hidden / 16) << half), (unsigned)tokens);
     expert_down<WG, MW, ST><<<grid, dim3(64 * MOE_MAX_K), 0, g->stream>>>(
         down->codes, (const ST *)down->scales, act, ids, weights, (int)k, (int)(down->rows / hidden), (int)hidden,

@@ -143,6 +143,18 @@ class Qwen3:
         check(lib.marin_qwen3_forward(self._h, cache._h, ids.ctypes.data, ids.size, logits.ctypes.data))
         return logits
 
+    def forward_rows(self, tokens, cache: "Qwen3Cache") -> np.ndarray:
+        """CausalLm::forward_rows (runtime/src/lib.rs:86-99): the logits after every token of a pass of at most 8,
+        [len(tokens)][vocab]."""
+        ids = np.ascontiguousarray(tokens, np.uint32).ravel()
+        rows = np.empty((ids.size, self.shape["vocab"]), np.float32)
+        check(lib.marin_qwen3_forward_rows(self._h, cache._h, ids.ctypes.data, ids.size, rows.ctypes.data))
+        return rows
+
+    def max_rows(self) -> int:
+        """CausalLm::max_rows (model/src/qwen3/gpu.rs:388-390)."""
+        return 8
+
     def generate(self, prompt, steps: int, cache: "Qwen3Cache") -> np.ndarray:
         ids = np.ascontiguousarray(prompt, np.uint32).ravel()
         out = np.zeros(steps, np.uint32)

@@ -141,6 +141,9 @@ void or_qwen3_synth_free(void *handle);
 /* Prompt pass then `steps` greedy tokens. tokens_out[steps]; gaps_out[steps] = top-1 minus top-2 logit of each step
  * (how far the choice is from a tie); top_ids/top_vals[steps * 5] (optional) the five best logits of each step.
  * Returns 0 on success. */
+/* The CPU baseline: seconds of one decode token of a model of this shape (constant weight codes, a filled cache of
+ * `ctx` positions in the config's KV format) through or_qwen3_forward on one thread; negative on failure. */
+double or_qwen3_time_token(const or_synth_config *cfg, size_t ctx);
 int or_qwen3_greedy(void *handle, const uint32_t *prompt, size_t prompt_len, size_t steps, uint32_t *tokens_out,
                     float *gaps_out, size_t prefill_chunk, uint32_t *top_ids, float *top_vals);
 

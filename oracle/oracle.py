@@ -349,3 +349,34 @@ def synth_greedy(shape: dict, seed: int, prompt, steps: int, kv_f16: bool = Fals
         return toks, gaps
     finally:
         lib.or_qwen3_synth_free(h)
+
+
+lib.or_qwen3_synth_model.restype = C.c_void_p
+lib.or_qwen3_synth_model.argtypes = [C.c_void_p]
+
+
+def synth_rows(shape: dict, seed: int, prompt, tokens, kv_f16: bool = False) -> np.ndarray:
+    """Logits after each of `tokens` (fed one at a time after the prompt) of the synthetic model ``shape``: the
+    reference's default forward_rows (runtime/src/lib.rs:86-99). [len(tokens)][vocab] f32."""
+    prompt = np.ascontiguousarray(prompt, np.uint32)
+    tokens = np.ascontiguousarray(tokens, np.uint32)
+    cfg = _SynthConfig(layers=shape["layers"], hidden=shape["hidden"], heads=shape["heads"],
+                       kv_heads=shape["kv_heads"], head_dim=shape["head_dim"], ffn=shape["ffn"],
+                       vocab=shape["vocab"], group=shape["group"], capacity=prompt.size + tokens.size + 1,
+                       eps=shape["eps"], theta=shape["theta"], tied=int(shape["tied"]), kv_f16=int(kv_f16),
+                       seed=seed)
+    h = lib.or_qwen3_synth_new(C.byref(cfg))
+    if not h:
+        raise ValueError("synthetic model could not be built")
+    try:
+        model = lib.or_qwen3_synth_model(h)
+        logits = np.zeros(shape["vocab"], np.float32)
+        if lib.or_qwen3_forward(model, prompt.ctypes.data, prompt.size, logits.ctypes.data):
+            raise ValueError("oracle prompt pass failed")
+        rows = np.zeros((tokens.size, shape["vocab"]), np.float32)
+        for i in range(tokens.size):
+            if lib.or_qwen3_forward(model, tokens[i:].ctypes.data, 1, rows[i].ctypes.data):
+                raise ValueError("oracle token pass failed")
+        return rows
+    finally:
+        lib.or_qwen3_synth_free(h)

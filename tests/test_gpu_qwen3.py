@@ -270,3 +270,31 @@ def test_batch_8_decode_at_8b_widths_matches_the_golden(gpu):
     for i, s in enumerate(seqs):
         compared += agree_until_a_near_tie(got[i].tolist(), s["tokens"], s["gaps"])
     assert compared >= len(seqs) * steps // 2
+
+
+@pytest.mark.parametrize("count", [2, 5, 8])
+def test_forward_rows_gives_every_rows_logits(gpu, count):
+    """CausalLm::forward_rows (runtime/src/lib.rs:86-99, model/src/qwen3/gpu.rs:212-236): one pass over the guessed
+    tokens returns the logits after each of them. Every row matches the oracle fed the same tokens one at a time
+    (the reference's default forward_rows) and the GPU's own one-token passes; the greedy continuation after it is
+    the one after feeding the tokens one by one; more than 8 tokens are refused and change nothing."""
+    g = golden("mini")
+    shape = g["shape"]
+    model = Qwen3(gpu, shape, seed=g["seed"])
+    prompt = g["prompt"][:24]
+    guesses = g["tokens"][:count]
+    cache = model.new_cache(64)
+    model.forward(prompt, cache)
+    rows = model.forward_rows(guesses, cache)
+    assert rows.shape == (count, shape["vocab"]) and len(cache) == len(prompt) + count
+    exp = o.synth_rows(shape, g["seed"], prompt, guesses)
+    for i in range(count):
+        assert np.abs(rows[i] - exp[i]).max() <= 1e-3 * (1 + np.abs(exp[i]).max()), i
+    one = model.new_cache(64)
+    model.forward(prompt, one)
+    singles = np.stack([model.forward([t], one) for t in guesses])
+    assert np.abs(rows - singles).max() < 1e-3
+    assert model.decode(4, cache).tolist() == model.decode(4, one).tolist()
+    with pytest.raises(m.Unsupported):
+        model.forward_rows(g["tokens"][:9], cache)
+    assert len(cache) == len(prompt) + count + 4
