@@ -52,6 +52,23 @@ __device__ __forceinline__ int total_key(float v) {
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
+// The four signed 8-bit limbs of four integers below 2^30 in magnitude: x = l3 2^24 + l2 2^16 + l1 2^8 + l0 with
+// l0..l2 in [-128, 127] (the balanced base-256 digits, unique), word l holding limb l of x0..x3 in bytes 0..3. With
+// y = x + 0x808080 the low three bytes of y are l0..l2 + 128 and y's top byte is l3, so the digits are byte gathers
+// (v_perm_b32) and one XOR of the sign bits.
+__device__ __forceinline__ void limbs4(int x0, int x1, int x2, int x3, uint32_t w[4]) {
+    const uint32_t y0 = (uint32_t)x0 + 0x808080u, y1 = (uint32_t)x1 + 0x808080u;
+    const uint32_t y2 = (uint32_t)x2 + 0x808080u, y3 = (uint32_t)x3 + 0x808080u;
+    const uint32_t a01 = __builtin_amdgcn_perm(y1, y0, 0x05010400u);  // y0.b0 y1.b0 y0.b1 y1.b1
+    const uint32_t a23 = __builtin_amdgcn_perm(y3, y2, 0x05010400u);
+    const uint32_t c01 = __builtin_amdgcn_perm(y1, y0, 0x07030602u);  // y0.b2 y1.b2 y0.b3 y1.b3
+    const uint32_t c23 = __builtin_amdgcn_perm(y3, y2, 0x07030602u);
+    w[0] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
+    w[1] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
+    w[2] = __builtin_amdgcn_perm(c23, c01, 0x05040100u) ^ 0x80808080u;
+    w[3] = __builtin_amdgcn_perm(c23, c01, 0x07060302u);
+}
+
 template <typename ST>
 __device__ __forceinline__ floatx4 scales4(const ST *p) {
     if constexpr (sizeof(ST) == 4) {
@@ -104,6 +121,8 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
     // A tile map (at most MAP_MAX entries) is loaded first, one entry per lane, and each item picks its entry with
     // a wave-uniform lane read: a per-item load of the map would sit behind the code windows already in flight and
     // wait for all of them.
+    // Without a map the activation row stands in: the ring's first addresses then wait for that one load, which
+    // measured faster than issuing the ring at once (the activations it races with feed the prologue).
     const int *map_p = in.tile_map ? in.tile_map : reinterpret_cast<const int *>(in.x);
     const int map_v = min(max(map_p[min(lane, max(in.map_count, 1) - 1)], 0), max(in.map_blocks, 1) - 1);
 
@@ -235,19 +254,13 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
         }
         const float up = ldexpf(1.0f, sh);
         u32x4 pk[4];
-        int lsum[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int l = 0; l < 4; ++l) pk[l] = (u32x4){0u, 0u, 0u, 0u};
+        for (int j = 0; j < 4; ++j) {
+            uint32_t w[4];
+            limbs4(__float2int_rn(v[4 * j] * up), __float2int_rn(v[4 * j + 1] * up), __float2int_rn(v[4 * j + 2] * up),
+                   __float2int_rn(v[4 * j + 3] * up), w);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            int xi = __float2int_rn(v[e] * up);
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const int lb = l == 3 ? xi : (int)(int8_t)(xi & 0xff);
-                pk[l][e / 4] |= ((uint32_t)lb & 0xffu) << (8 * (e % 4));
-                lsum[l] += lb;
-                xi = (xi - lb) >> 8;
-            }
+            for (int l = 0; l < 4; ++l) pk[l][j] = w[l];
         }
         if (wr < DW * S) {
 #pragma unroll
@@ -260,7 +273,9 @@ __global__ __launch_bounds__(64 * DW) void gemv_decode(const uint8_t *__restrict
             // stored nibbles are code + 8: the group's sum of each limb column, times 8, comes off the sums
 #pragma unroll
             for (int l = 0; l < 4; ++l) {
-                int sm = lsum[l];
+                int sm = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sm = __builtin_amdgcn_sdot4((int)pk[l][j], 0x01010101, sm, false);
                 sm += dpp_i<0xB1>(sm);
                 sm += dpp_i<0x4E>(sm);
                 if constexpr (WG == 2) sm += dpp_i<0x141>(sm);

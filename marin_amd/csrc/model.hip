@@ -62,10 +62,11 @@ __device__ __forceinline__ void embed_row(const uint8_t *__restrict__ codes, con
 __global__ __launch_bounds__(512) void advance(unsigned long long *best, uint32_t *ids, uint32_t *tokens_out,
                                                uint32_t *state, const uint8_t *__restrict__ codes,
                                                const float *__restrict__ scales, float *__restrict__ hidden, int cols,
-                                               int group) {
+                                               int group, uint32_t vocab) {
     __shared__ uint32_t id_s;
     if (threadIdx.x == 0) {
-        const uint32_t id = 0xffffffffu - (uint32_t)(*best & 0xffffffffull);
+        // an empty choice word (no head block wrote one) would decode to 0xffffffff: the id is kept inside the table
+        const uint32_t id = min(0xffffffffu - (uint32_t)(*best & 0xffffffffull), vocab - 1);
         *best = 0ull;
         ids[0] = id;
         tokens_out[state[2]] = id;
@@ -126,11 +127,11 @@ __global__ void embed_device_ids(const uint8_t *__restrict__ codes, const float 
 __global__ __launch_bounds__(512) void advance_batch(unsigned long long *best, uint32_t *tokens_out, uint32_t *state,
                                                      int batch, const uint8_t *__restrict__ codes,
                                                      const float *__restrict__ scales, float *__restrict__ hidden,
-                                                     int cols, int group) {
+                                                     int cols, int group, uint32_t vocab) {
     __shared__ uint32_t id_s;
     const int b = blockIdx.x;
     if (threadIdx.x == 0) {
-        const uint32_t id = 0xffffffffu - (uint32_t)(best[b] & 0xffffffffull);
+        const uint32_t id = min(0xffffffffu - (uint32_t)(best[b] & 0xffffffffull), vocab - 1);
         best[b] = 0ull;
         tokens_out[(size_t)state[2 * batch + b] * batch + b] = id;
         state[b] += 1;
@@ -598,7 +599,7 @@ static void decode_step(marin_qwen3 *m, marin_qwen3_cache *c, size_t host_ctx) {
     marin_gpu *g = m->gpu;
     advance<<<1, 512, 0, g->stream>>>(c->best, c->ids, c->tokens_out, c->state, m->embed->codes,
                                       (const float *)m->embed->scales, c->hidden, (int)m->cfg.hidden,
-                                      (int)m->cfg.group);
+                                      (int)m->cfg.group, (uint32_t)m->cfg.vocab);
     g->launched();
     pass(m, io_of(c, 1), c->kv->capacity, host_ctx);
 }
@@ -817,7 +818,7 @@ static void batch_step(marin_qwen3 *m, marin_qwen3_batch *b) {
     marin_gpu *g = m->gpu;
     advance_batch<<<(unsigned)b->seqs.size(), 512, 0, g->stream>>>(
         b->best, b->tokens_out, b->state, (int)b->seqs.size(), m->embed->codes, (const float *)m->embed->scales,
-        b->hidden, (int)m->cfg.hidden, (int)m->cfg.group);
+        b->hidden, (int)m->cfg.hidden, (int)m->cfg.group, (uint32_t)m->cfg.vocab);
     g->launched();
     pass(m, io_of(b), b->capacity, 0);
 }
