@@ -786,8 +786,9 @@ __device__ __forceinline__ void merge_records(__amdgpu_buffer_rsrc_t prs, int re
 template <int F, int LPP, bool BF16IO, int R, bool FUSE, int U>
 __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const void *__restrict__ qv, AttnFuse fuse, const uint64_t *__restrict__ tables, size_t table_stride,
-    const uint32_t *__restrict__ ctx_lens, KvGeom geom, int heads, int kv_heads, int chunk, int splits, float scale,
-    float *__restrict__ part, int part_bytes, uint32_t *__restrict__ counters, void *__restrict__ out) {
+    int table_len, const uint8_t *__restrict__ zero_row, const uint32_t *__restrict__ ctx_lens, KvGeom geom,
+    int heads, int kv_heads, int chunk, int splits, float scale, float *__restrict__ part, int part_bytes,
+    uint32_t *__restrict__ counters, void *__restrict__ out) {
     constexpr int NW = DEC_NW, NT = 64 * NW;
     constexpr int HMAX = 8 * LPP;  // head values covered by the lanes of one position
     constexpr int PPW = 64 / LPP;  // positions per wave step
@@ -797,8 +798,18 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const int hd = (int)geom.head_dim;
     const int group = heads / kv_heads;
     const int kvh = blockIdx.y, b = blockIdx.z, split = blockIdx.x;
-    const int ctx = (int)ctx_lens[b];
     const int first = split * chunk;
+    const uint64_t *table = tables + (size_t)b * table_stride;
+    // ---- 1. page addresses of this lane's positions, first of all loads and before the context length is known
+    // (an index past the table is clamped; entries past the context are never dereferenced)
+    uint64_t pg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int p = first + wave * PPW + slot + u * STEP;
+        pg[u] = table[min(p >> (int)geom.page_shift, table_len - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int ctx = (int)ctx_lens[b];
     if (first >= ctx) return;
     const int count = min(chunk, ctx - first);
     const int used = (ctx + chunk - 1) / chunk;
@@ -807,7 +818,6 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const size_t es = F == MARIN_KV_F32 ? 4 : 2;
     const uint64_t head_off = (uint64_t)kvh * geom.head_bytes + geom.layer_offset;
     const uint32_t pmask = (1u << geom.page_shift) - 1u;
-    const uint64_t *table = tables + (size_t)b * table_stride;
     const int newpos = ctx - 1;
     const bool owns_new = FUSE && newpos >= first && newpos < first + count;
 
@@ -819,14 +829,6 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     __shared__ float hm_s[R][DEC_MAX_SPLITS], hl_s[R][DEC_MAX_SPLITS];
     __shared__ int last_s;
 
-    // ---- 1. page addresses of this lane's positions (clamped to the chunk's last), first of all loads
-    uint64_t pg[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int p = first + min(wave * PPW + slot + u * STEP, count - 1);
-        pg[u] = table[p >> geom.page_shift];
-    }
-    __builtin_amdgcn_sched_barrier(0);
     // ---- 2. the query inputs (FUSE: raw q heads with the cos/sin of the new position, and the raw new key and value
     // where this chunk holds them), issued behind the page addresses so waiting for those does not wait for these
     constexpr int QPW = (R + NW - 1) / NW;  // q heads per wave
@@ -866,10 +868,13 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     Raw8<F> kr[U], vr[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint32_t p = (uint32_t)(first + min(wave * PPW + slot + u * STEP, count - 1));
+        // positions past the chunk read the zero row (weighed 0 below) rather than an entry never mapped
+        const int rel = wave * PPW + slot + u * STEP;
+        const uint32_t p = (uint32_t)(first + rel);
+        const bool in = rel < count;
         const uint8_t *row = reinterpret_cast<const uint8_t *>(pg[u] + head_off + (uint64_t)(p & pmask) * hd * es);
-        load_raw<F, true>(row, dl, hd, kr[u]);
-        load_raw<F, true>(row + geom.value_offset, dl, hd, vr[u]);
+        load_raw<F, true>(in ? row : zero_row, dl, hd, kr[u]);
+        load_raw<F, true>(in ? row + geom.value_offset : zero_row, dl, hd, vr[u]);
     }
     __builtin_amdgcn_sched_barrier(0);
     ATT_T(1);
@@ -1210,12 +1215,14 @@ static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int c
     auto kern = attention_decode<F, LPP, BF16IO, R, FUSE, U>;
     if (t0)
         hipExtLaunchKernelGGL(kern, grid, dim3(64 * DEC_NW), 0u, g->stream, t0, t1, 0u, a.q, a.fuse, a.tables,
-                              a.table_stride, a.ctx, a.geom, (int)a.heads, (int)a.kv_heads, chunk, splits, scale,
-                              a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+                              a.table_stride, (int)a.table_len, (const uint8_t *)g->zero_row, a.ctx, a.geom,
+                              (int)a.heads, (int)a.kv_heads, chunk, splits, scale, a.partials,
+                              (int)(a.partial_floats * 4), a.counters, a.out);
     else
-        kern<<<grid, dim3(64 * DEC_NW), 0, g->stream>>>(a.q, a.fuse, a.tables, a.table_stride, a.ctx, a.geom,
-                                                        (int)a.heads, (int)a.kv_heads, chunk, splits, scale,
-                                                        a.partials, (int)(a.partial_floats * 4), a.counters, a.out);
+        kern<<<grid, dim3(64 * DEC_NW), 0, g->stream>>>(a.q, a.fuse, a.tables, a.table_stride, (int)a.table_len,
+                                                        (const uint8_t *)g->zero_row, a.ctx, a.geom, (int)a.heads,
+                                                        (int)a.kv_heads, chunk, splits, scale, a.partials,
+                                                        (int)(a.partial_floats * 4), a.counters, a.out);
 }
 
 template <int F, int LPP, int R, int U>
@@ -1304,6 +1311,9 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
     const int dchunk = decode_kernel_fits(a) ? decode_chunk(a, g->cu_count, dsplits) : 0;
     if (dchunk) {
         if (a.fuse.qkv && !a.fuse.rope) unsupported("fused decode attention without a RoPE table", 1, 0);
+        if (a.table_len == 0 || a.table_len > 0x7fffffffu) shape("decode attention page table entries", 1, a.table_len);
+        if (a.geom.head_dim * kv_elem_bytes((marin_kv_format)a.geom.format) > 4096)
+            unsupported("decode attention row bytes", 4096, a.geom.head_dim * kv_elem_bytes((marin_kv_format)a.geom.format));
         if (a.batch * a.kv_heads > a.counter_count) shape("attention chunk counters", a.batch * a.kv_heads, a.counter_count);
         const size_t dneed = a.batch * a.heads * (size_t)dsplits * (size_t)rec_floats((int)a.geom.head_dim);
         if (dsplits > 1 && dneed > a.partial_floats) shape("attention partial records (floats)", dneed, a.partial_floats);
@@ -1596,6 +1606,7 @@ marin_status marin_attention(marin_gpu *g, const marin_buffer *q, marin_kv *kv, 
             a.out = (float *)out->data + t0 * heads * hd;
             a.tables = kv->page_ptrs;
             a.table_stride = 0;
+            a.table_len = std::max<size_t>(kv->pool.limit, 1);
             a.ctx = kv->ctx;
             a.batch = 1;
             a.tokens = nt;
@@ -1746,6 +1757,7 @@ marin_status marin_paged_attention_batch(marin_gpu *g, const marin_buffer *q, ma
         a.out = out->data;
         a.tables = p->tables;
         a.table_stride = table_stride;
+        a.table_len = table_stride;
         a.ctx = p->ctx;
         a.batch = batch;
         a.tokens = 1;

@@ -76,6 +76,7 @@ struct AttentionArgs {
     AttnFuse fuse;   // fuse.qkv set: q/k norm + RoPE + the store of the new keys/values happen in the kernel
     const uint64_t *tables;
     size_t table_stride;
+    size_t table_len = 0;  // entries of one sequence's table (the one-token kernel reads its entries before ctx)
     const uint32_t *ctx;  // device
     size_t batch, tokens, heads, kv_heads;
     KvGeom geom;

@@ -141,6 +141,8 @@ struct marin_gpu {
     // carry on with harmless values; the next blocking call (synchronize, download) reports it and clears it.
     uint32_t *fault = nullptr;
     void check_fault();
+    // 4 KiB of zeros on the device: the row the one-token attention reads for positions past a context.
+    void *zero_row = nullptr;
     // Gpu::set_fast_attention (crates/cuda/src/attention.rs:81-86): prompt passes over an f16 cache use the
     // matrix-core attention when set (the default; MARIN_NO_FA=1 in the environment clears it at creation).
     bool fast_attention = true;

@@ -109,6 +109,7 @@ void marin_gpu::destroy() {
     (void)hipStreamSynchronize(stream);
     if (work) (void)hipFree(work);
     if (fault) (void)hipFree(fault);
+    if (zero_row) (void)hipFree(zero_row);
     if (pinned) (void)hipHostFree(pinned);
     for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(stream);
@@ -237,9 +238,12 @@ marin_status marin_gpu_new(marin_gpu **out) {
         }
         e = hipMalloc((void **)&g->fault, 256);
         if (e == hipSuccess) e = hipMemset(g->fault, 0, 256);
+        if (e == hipSuccess) e = hipMalloc(&g->zero_row, 4096);
+        if (e == hipSuccess) e = hipMemset(g->zero_row, 0, 4096);
         if (e != hipSuccess) {
             (void)hipStreamDestroy(g->stream);
             if (g->fault) (void)hipFree(g->fault);
+            if (g->zero_row) (void)hipFree(g->zero_row);
             delete g;
             hip_check(e, "hipMalloc (fault word)");
         }

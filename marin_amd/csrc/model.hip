@@ -349,6 +349,7 @@ static void pass(marin_qwen3 *m, const PassIo &io, size_t max_ctx, size_t host_c
         a.fuse.eps = cfg.rms_eps;
         a.tables = io.tables;
         a.table_stride = io.table_stride;
+        a.table_len = io.table_stride ? io.table_stride : std::max<size_t>(io.kv->pool.limit, 1);
         a.ctx = io.ctx_lens;
         a.batch = io.batch;
         a.tokens = io.tokens;
