@@ -29,6 +29,27 @@ import time
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def traffic_of(mode: str, key: str):
+    """HBM bytes per launch of `key` in `mode` from the committed rocprofv3 counter runs (profiles/traffic.json:
+    FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the copy probe's calibration), or None."""
+    if not os.path.exists(TRAFFIC):
+        return None
+    t = json.load(open(TRAFFIC))
+    entry = t.get("modes", {}).get(mode, {}).get(key)
+    if entry is None and mode == "decode":
+        entry = t.get("kernels", {}).get(key)
+    return entry["hbm_bytes_per_launch"] if entry else None
+
+
+def counter_marker(gpu) -> None:
+    """Brackets the dispatches of a `--counters` run: two launches of the copy probe on 1 MiB, which the counter
+    summaries (profiles/traffic.json) use to find the region between them."""
+    gpu.synchronize()
+    gpu.probe_copy(1 << 20, 1)
+    gpu.synchronize()
 
 
 def layer_params(shape: dict) -> int:
@@ -135,6 +156,14 @@ def bench_moe(m, args) -> int:
         act = gpu.zeros(batch * K * F)
         out = gpu.zeros(batch * H)
         xb = gpu.upload(x.ravel())
+        if args.counters:
+            # eager (MARIN_NO_GRAPH): one untimed stack then one timed stack of the L layers between the markers
+            counter_marker(gpu)
+            gpu.moe_stack_time(gate_ups, downs, xb, norm, 1e-6, ids, wts, batch, E, K, act, out, reps=1)
+            counter_marker(gpu)
+            print(json.dumps({"counters": "moe", "batch": batch, "stacks": 2, "layers": L,
+                              "experts_read_per_layer": sum(len(np.unique(i)) for i in results[batch]["ids"]) / L}))
+            return 0
         sec = gpu.moe_stack_time(gate_ups, downs, xb, norm, 1e-6, ids, wts, batch, E, K, act, out,
                                  reps=max(args.steps // 16, 5))
         reps = max(args.steps // 16, 5)
@@ -171,9 +200,10 @@ def bench_moe(m, args) -> int:
         "config": {"workload": "qwen3-30b-a3b expert FFN stack (48 layers, 128 experts x ffn 768, top-8, hidden "
                                "2048), batch 1; batch 8 under batches; each layer's decode attention at 2048 "
                                "positions (32 q / 4 kv heads) timed beside it (attention_us_per_layer)", **c},
-        "roofline": {"bound": "hbm", "kernel": "gemv_decode (tile-mapped) + expert_down", "achieved": r1["GBps"],
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(r1["GBps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": "gemv_decode (tile-mapped) + expert_down, per layer",
+                     "achieved": r1["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(r1["GBps"] / HBM_PEAK_GBPS, 4), "traffic": traffic_of("moe", "expert layer"),
+                     "bytes_per_launch": round(r1["algorithmic_bytes_per_stack"] / L)},
         "batches": results,
     }
     print(json.dumps(line), flush=True)
@@ -185,7 +215,7 @@ def bench_batch(m, args) -> int:
     through its own cache, then decoded together (one greedy token per sequence per step: every product over the N
     tokens, one attention launch over all sequences, the step replayed as a HIP graph). value = N x K / wall seconds
     of K timed steps."""
-    from marin_amd.qwen3 import SHAPES, Qwen3
+    from marin_amd.qwen3 import SHAPES, Qwen3, weight_bytes
 
     shape = SHAPES["qwen3-8b"]
     fmt = {"f32": m.KvFormat.F32, "f16": m.KvFormat.F16, "bf16": m.KvFormat.BF16}[args.kv]
@@ -202,6 +232,13 @@ def bench_batch(m, args) -> int:
     gpu.synchronize()
     prefill_s = time.perf_counter() - t
     print(f"[bench] {B} prompts in {prefill_s:.2f}s", file=sys.stderr, flush=True)
+    if args.counters:
+        batch.decode(1)  # one step first, so the counted step is not the one that opens new KV slabs
+        counter_marker(gpu)
+        batch.decode(1)
+        counter_marker(gpu)
+        print(json.dumps({"counters": "batch", "batch": B, "steps": 1}))
+        return 0
     batch.decode(args.warmup)
     gpu.synchronize()
     t = time.perf_counter()
@@ -211,6 +248,12 @@ def bench_batch(m, args) -> int:
     tok_s = B * args.steps / wall
     print(f"[bench] batch {B}: {args.steps} steps in {wall * 1e3:.1f} ms: {tok_s:.1f} tok/s aggregate, "
           f"{wall / args.steps * 1e3:.3f} ms per step", file=sys.stderr, flush=True)
+    # algorithmic bytes of one step: the weights once, plus every sequence's cached keys and values at the mean context
+    # of the timed steps
+    kv_el = {"f32": 4, "f16": 2, "bf16": 2}[args.kv]
+    mean_ctx = args.prompt + args.warmup + args.steps / 2
+    step_bytes = weight_bytes(shape) + B * mean_ctx * shape["layers"] * shape["kv_heads"] * shape["head_dim"] * 2 * kv_el
+    step_gbps = step_bytes / (wall / args.steps) / 1e9
     line = {
         "metric": f"decode tok/s Qwen3-8B-shape int8 bs={B} (aggregate over the batch)",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -220,7 +263,10 @@ def bench_batch(m, args) -> int:
         "config": {"workload": f"qwen3-8b int8-g128 greedy decode, batch {B}, each sequence after a "
                                f"{args.prompt}-token prompt", "prompt": args.prompt, "batch": B, "kv_format": args.kv,
                    "layers": shape["layers"], "hidden": shape["hidden"], "ffn": shape["ffn"], "vocab": shape["vocab"]},
-        "weight_GBps": round(7.8046e9 / (wall / args.steps) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "one decode step (every launch of the step)", "achieved": round(step_gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_of("batch", "decode step"), "bytes_per_launch": round(step_bytes)},
+        "weight_GBps": round(weight_bytes(shape) / (wall / args.steps) / 1e9, 1),
         "prefill_tok_s": round(B * args.prompt / prefill_s, 1),
         "first_tokens": toks[:, :4].tolist(),
     }
@@ -243,6 +289,18 @@ def bench_linear(m, args) -> int:
     gpu = m.Gpu()
     rng = np.random.default_rng(args.seed)
     shapes = [(4096, 4096), (4096, 12288), (12288, 4096), (4096, 151936)]  # (K, N)
+    if args.counters:
+        # one eager product per int8 M = 1 shape, in this order, each between two markers, for rocprofv3 counter runs
+        for K, N in shapes:
+            w = gpu.quantized_synthetic(N, K, 128, args.seed, 0)
+            x = gpu.typed(m.Dtype.BF16, host=_bf16(rng.standard_normal((1, K))))
+            out = gpu.typed(m.Dtype.BF16, N)
+            counter_marker(gpu)
+            gpu.matmul_quant_bf16(w, x, 1, out)
+            counter_marker(gpu)
+            del w
+        print(json.dumps({"counters": "linear", "order": [f"int8 K={K} N={N} M=1" for K, N in shapes]}))
+        return 0
     cases = []
     for bits in (8, 4):
         for K, N in shapes:
@@ -277,8 +335,10 @@ def bench_linear(m, args) -> int:
         "data": "synthetic (int8: N(0,0.02) weights quantized on device; int4: random codes; bf16 N(0,1) inputs)",
         "config": {"workload": "config 1: (K, N) in {(4096,4096), (4096,12288), (12288,4096), (4096,151936)}, "
                                "M in {1, 4, 8}, int8 and int4 group 128, bf16 in and out; value over int8 M=1"},
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": "gemv_decode (int8, M = 1, the four shapes)", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_of("linear", "int8 M=1, four shapes"),
+                     "bytes_per_launch": round(tot_b / len(one))},
         "cases": cases,
     }
     print(json.dumps(line), flush=True)
@@ -316,6 +376,12 @@ def bench_paged(m, args) -> int:
             at += 1
     q = gpu.typed(m.Dtype.BF16, host=_bf16(rng.standard_normal((batch, heads, hd))))
     out = gpu.typed(m.Dtype.BF16, batch * heads * hd)
+    if args.counters:
+        counter_marker(gpu)
+        pools[0].attention(q, tables, ctx, heads, out)
+        counter_marker(gpu)
+        print(json.dumps({"counters": "paged", "order": ["attention_decode", "attention_decode_merge"]}))
+        return 0
     for i in range(2 * npools):
         pools[i % npools].attention(q, tables, ctx, heads, out)
     gpu.synchronize()
@@ -337,8 +403,9 @@ def bench_paged(m, args) -> int:
                 f"pool ({npools * total * page_bytes / 1e6:.0f} MB) used in turn)",
         "config": {"workload": "config 2: batch 16, 32 q / 8 kv heads, head_dim 128, 16-position pages, contexts "
                                "uniform in [512, 8192], shuffled page tables from one pool", "contexts": ctx.tolist()},
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": "attention_decode + attention_decode_merge", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_of("paged", "attention call"), "bytes_per_launch": nbytes},
         "bytes_per_call": nbytes,
     }
     print(json.dumps(line), flush=True)
@@ -372,10 +439,13 @@ def main() -> int:
     ap.add_argument("--moe", action="store_true",
                     help="config 4 instead: the Qwen3-30B-A3B-shaped expert FFN stack at batch 1 and 8 (grouped-expert "
                          "GEMV GB/s), one JSON line")
+    ap.add_argument("--counters", action="store_true",
+                    help="for rocprofv3 --pmc runs: set the mode's inputs up, then launch its measured work once, "
+                         "eagerly, between two copy-probe markers, and exit (no timing, no JSON result line)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's kernels one by one instead of replaying a HIP graph (for tracers)")
     args = ap.parse_args()
-    if args.no_graph:
+    if args.no_graph or args.counters:
         os.environ["MARIN_NO_GRAPH"] = "1"
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -420,6 +490,13 @@ def main() -> int:
     prefill_s = time.perf_counter() - t
     print(f"[bench] weights {build_s:.1f}s, prefill {prefill_s:.2f}s", file=sys.stderr, flush=True)
 
+    if args.counters:
+        model.decode(1, cache)  # one step first, so the counted step is not the one that opens a new KV slab
+        counter_marker(gpu)
+        model.decode(1, cache)
+        counter_marker(gpu)
+        print(json.dumps({"counters": "decode", "steps": 1}))
+        return 0
     model.decode(args.warmup, cache)
     gpu.synchronize()
     m0 = gpu.mark()
@@ -439,10 +516,10 @@ def main() -> int:
         recs += model.profile_launches(cache)
     kernels = {}
     for kind, name, nbytes, sec in recs:
-        if kind == 0:
+        if kind == 0 and not name:
             continue
-        k = kernels.setdefault(name, {"kind": "product" if kind == 1 else "attention", "launches": 0, "bytes": 0.0,
-                                      "seconds": 0.0})
+        k = kernels.setdefault(name, {"kind": ["attention merge", "product", "attention"][kind], "launches": 0,
+                                      "bytes": 0.0, "seconds": 0.0})
         k["launches"] += 1
         k["bytes"] += nbytes
         k["seconds"] += sec
@@ -467,12 +544,7 @@ def main() -> int:
     for name, k in sorted(summary.items(), key=lambda kv: -kv[1]["us_per_step"]):
         print(f"[bench] {name}: {k['launches_per_step']} launches/step, {k['mean_launch_us']:.2f} us each, "
               f"{k['GBps']:.0f} GB/s, {k['us_per_step']:.0f} us/step", file=sys.stderr, flush=True)
-    traffic = None
-    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        t = json.load(open(tpath)).get("kernels", {}).get(dom)
-        if t:
-            traffic = t["hbm_bytes_per_launch"]
+    traffic = traffic_of("decode", dom)
 
     line = {
         "metric": "decode tok/s Qwen3-8B-shape int8 bs=1; GEMV+attn HBM GB/s vs 8 TB/s peak",
