@@ -42,11 +42,15 @@ struct Raw8 {
 };
 
 // Values d .. d + 7 of a row (VEC: d + 8 <= head_dim and 16-byte aligned; else element by element, zero past hd).
-template <int F, bool VEC>
+// NT: nontemporal (streaming) loads, for rows read once per launch.
+template <int F, bool VEC, bool NT = false>
 __device__ __forceinline__ void load_raw(const uint8_t *row, int d, int hd, Raw8<F> &r) {
     constexpr int ES = F == MARIN_KV_F32 ? 4 : 2;
     const uintptr_t base = (uintptr_t)row + (uintptr_t)d * ES;
-    if constexpr (VEC) {
+    if constexpr (VEC && NT) {
+        r.w[0] = __builtin_nontemporal_load((g_u32x4 *)base);
+        if constexpr (F == MARIN_KV_F32) r.w[1] = __builtin_nontemporal_load((g_u32x4 *)(base + 16));
+    } else if constexpr (VEC) {
         r.w[0] = *(g_u32x4 *)base;
         if constexpr (F == MARIN_KV_F32) r.w[1] = *(g_u32x4 *)(base + 16);
     } else {
@@ -648,9 +652,6 @@ __device__ __forceinline__ void finish_head_cs(const HeadIn &h, int hd, float ep
     }
 }
 
-#ifndef ATTN_MERGE_KERNEL
-#define ATTN_MERGE_KERNEL 1
-#endif
 constexpr int DEC_NW = 4;           // waves per workgroup
 constexpr int DEC_MAX_SPLITS = 64;  // chunks the last workgroup merges (a lane of one wave each)
 
@@ -788,7 +789,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const void *__restrict__ qv, AttnFuse fuse, const uint64_t *__restrict__ tables, size_t table_stride,
     int table_len, const uint8_t *__restrict__ zero_row, const uint32_t *__restrict__ ctx_lens, KvGeom geom,
     int heads, int kv_heads, int chunk, int splits, float scale, float *__restrict__ part, int part_bytes,
-    uint32_t *__restrict__ counters, void *__restrict__ out) {
+    void *__restrict__ out) {
     constexpr int NW = DEC_NW, NT = 64 * NW;
     constexpr int HMAX = 8 * LPP;  // head values covered by the lanes of one position
     constexpr int PPW = 64 / LPP;  // positions per wave step
@@ -800,6 +801,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const int kvh = blockIdx.y, b = blockIdx.z, split = blockIdx.x;
     const int first = split * chunk;
     const uint64_t *table = tables + (size_t)b * table_stride;
+    ATT_T(6);
     // ---- 1. page addresses of this lane's positions, first of all loads and before the context length is known
     // (an index past the table is clamped; entries past the context are never dereferenced)
     uint64_t pg[U];
@@ -822,12 +824,14 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     const bool owns_new = FUSE && newpos >= first && newpos < first + count;
 
     ATT_T(0);
+    // partials: every lane group's (R > 4: every pair of lane groups 32 lanes apart) max, sum and weighted values
+    constexpr int PRE = R > 4 ? 1 : 0;
+    constexpr int NP = NW * (PPW >> PRE);
     __shared__ float q_s[R][HMAX];
     __shared__ float new_s[2][HMAX];  // the new key (normalized and rotated) and value
-    __shared__ float wm_s[NW][R], wl_s[NW][R];
-    __shared__ float wacc_s[NW][R][HMAX];
-    __shared__ float hm_s[R][DEC_MAX_SPLITS], hl_s[R][DEC_MAX_SPLITS];
-    __shared__ int last_s;
+    __shared__ float pacc_s[NP][R][HMAX];
+    __shared__ float pm_s[R][NP], pl_s[R][NP], pw_s[R][NP];
+    __shared__ float rm_s[R], rl_s[R];
 
     // ---- 2. the query inputs (FUSE: raw q heads with the cos/sin of the new position, and the raw new key and value
     // where this chunk holds them), issued behind the page addresses so waiting for those does not wait for these
@@ -849,17 +853,31 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
             for (int k = 0; k < 4; ++k) vin[k] = lane + 64 * k < hd ? vsrc[lane + 64 * k] : 0.0f;
         }
     } else {
-        // this lane's 8 values of every q head of the kv head, straight into registers
+        // this lane's 8 values of every q head of the kv head, straight into registers (16-byte loads: hd is a
+        // multiple of 8, so a lane's 8 values are aligned)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int rr = min(r, group - 1);
             const size_t at = ((size_t)b * heads + kvh * group + rr) * hd + dl;
+            float v[8];
+            if constexpr (BF16IO) {
+                const u32x4 w = *(g_u32x4 *)(uintptr_t)(reinterpret_cast<const uint16_t *>(qv) + at);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float v = BF16IO ? bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(qv)[at + i])
-                                       : reinterpret_cast<const float *>(qv)[at + i];
-                q[r][i] = (r < group && d + i < hd) ? v : 0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    v[2 * i] = __uint_as_float(w[i] << 16);
+                    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+                }
+            } else {
+                const uintptr_t base = (uintptr_t)(reinterpret_cast<const float *>(qv) + at);
+                const u32x4 w0 = *(g_u32x4 *)base, w1 = *(g_u32x4 *)(base + 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = __uint_as_float(w0[i]);
+                    v[4 + i] = __uint_as_float(w1[i]);
+                }
             }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[r][i] = (r < group && d + i < hd) ? v[i] : 0.0f;
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // the query loads stay ahead of the row loads
@@ -873,8 +891,16 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
         const uint32_t p = (uint32_t)(first + rel);
         const bool in = rel < count;
         const uint8_t *row = reinterpret_cast<const uint8_t *>(pg[u] + head_off + (uint64_t)(p & pmask) * hd * es);
-        load_raw<F, true>(in ? row : zero_row, dl, hd, kr[u]);
-        load_raw<F, true>(in ? row + geom.value_offset : zero_row, dl, hd, vr[u]);
+        load_raw<F, true, true>(in ? row : zero_row, dl, hd, kr[u]);
+    }
+    // the value rows after every key row: the scores can start while the values are still in flight
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int rel = wave * PPW + slot + u * STEP;
+        const uint32_t p = (uint32_t)(first + rel);
+        const bool in = rel < count;
+        const uint8_t *row = reinterpret_cast<const uint8_t *>(pg[u] + head_off + (uint64_t)(p & pmask) * hd * es);
+        load_raw<F, true, true>(in ? row + geom.value_offset : zero_row, dl, hd, vr[u]);
     }
     __builtin_amdgcn_sched_barrier(0);
     ATT_T(1);
@@ -971,11 +997,11 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     }
 
     ATT_T(3);
-    // ---- 6. the lane groups of a wave combined pairwise (partners LPP, 2 LPP, ... lanes apart; both lanes of a pair
-    // compute the same lower-then-upper combination), then the waves through LDS; each step rescales both sides to
-    // the larger maximum
+    // ---- 6. the partials of the workgroup (R > 4: lane groups 32 lanes apart combined in registers first, both
+    // lanes of a pair computing the same lower-then-upper combination) to LDS; then per row the maximum over the
+    // partials, each partial's weight and the weighted sum of the sums, every sum in a fixed order
 #pragma unroll
-    for (int o = LPP; o < 64; o <<= 1) {
+    for (int o = 64 >> PRE; o < 64; o <<= 1) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float m0, m1, l0, l1;
@@ -994,43 +1020,49 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
             mrow[r] = mn;
         }
     }
-    if (slot == 0) {
+    if (slot < (PPW >> PRE)) {
+        const int pi = wave * (PPW >> PRE) + slot;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) wacc_s[wave][r][d + i] = acc[r][i];
+            for (int i = 0; i < 8; ++i) pacc_s[pi][r][d + i] = acc[r][i];
             if (sub == 0) {
-                wm_s[wave][r] = mrow[r];
-                wl_s[wave][r] = lrow[r];
+                pm_s[r][pi] = mrow[r];
+                pl_s[r][pi] = lrow[r];
             }
         }
     }
     __syncthreads();
+    if (threadIdx.x < R) {
+        const int r = threadIdx.x;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) mx = fmaxf(mx, pm_s[r][p]);
+        float l = 0.0f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float w = pm_s[r][p] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pm_s[r][p] - mx);
+            pw_s[r][p] = w;
+            l += w * pl_s[r][p];
+        }
+        rm_s[r] = mx;
+        rl_s[r] = l;
+    }
+    __syncthreads();
     ATT_T(4);
-    // the workgroup's (max, sum, weighted values) of row r, value e: the waves in order
-    auto combine = [&](int r, int e, float &m_out, float &l_out) {
-        float mn = -INFINITY;
+    // the workgroup's weighted values of row r, values e .. e + 3 (e a multiple of 4)
+    auto combine4 = [&](int r, int e) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int w = 0; w < NW; ++w) mn = fmaxf(mn, wm_s[w][r]);
-        float a = 0.0f, l = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float f = wm_s[w][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(wm_s[w][r] - mn);
-            a += wacc_s[w][r][e] * f;
-            l += wl_s[w][r] * f;
+        for (int p = 0; p < NP; ++p) {
+            const float w = pw_s[r][p];
+            const float4 x = *reinterpret_cast<const float4 *>(&pacc_s[p][r][e]);
+            a.x += w * x.x;
+            a.y += w * x.y;
+            a.z += w * x.z;
+            a.w += w * x.w;
         }
-        m_out = mn;
-        l_out = l;
         return a;
-    };
-    auto write_out = [&](int r, int e, float v) {
-        const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
-        if constexpr (BF16IO) {
-            const unsigned u = __float_as_uint(v);
-            reinterpret_cast<uint16_t *>(out)[at] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-        } else {
-            reinterpret_cast<float *>(out)[at] = v;
-        }
     };
 
     // the new key and value, stored for later steps (this launch took them from LDS); stored here, after every
@@ -1043,54 +1075,43 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
         }
     }
     if (used == 1) {
-        for (int o = threadIdx.x; o < group * hd; o += NT) {
-            float m, l;
-            const float a = combine(o / hd, o % hd, m, l);
-            write_out(o / hd, o % hd, a / l);
+        for (int o = threadIdx.x; o < group * (hd / 4); o += NT) {
+            const int r = o / (hd / 4), e = 4 * (o % (hd / 4));
+            const float4 a = combine4(r, e);
+            const float inv = 1.0f / rl_s[r];
+            const float v[4] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv};
+            const size_t at = ((size_t)b * heads + kvh * group + r) * hd + e;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (BF16IO) {
+                    const unsigned u = __float_as_uint(v[j]);
+                    reinterpret_cast<uint16_t *>(out)[at + j] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+                } else {
+                    reinterpret_cast<float *>(out)[at + j] = v[j];
+                }
+            }
         }
         return;
     }
 
-    // ---- 7. this chunk's record per row: [max, sum, 0, 0, values, pad], 16-byte agent-coherent stores
+    // ---- 7. this chunk's record per row, [max, sum, 0, 0, values, pad] in 16-byte stores; attention_decode_merge
+    // combines the records after this launch
     const int RS = rec_floats(hd);
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, part_bytes, 0x00020000);
-    constexpr int SC1 = 16;  // the device-scope bit of the cache policy
-    auto rec_off = [&](int r, int sp) {
-        return (int)(((((size_t)b * heads + kvh * group + r) * splits) + sp) * (size_t)RS * 4);
-    };
     for (int o = threadIdx.x; o < group * (RS / 4); o += NT) {
         const int r = o / (RS / 4), c4 = o % (RS / 4);
         u32x4 v;
-        float m, l;
         if (c4 == 0) {
-            (void)combine(r, 0, m, l);
-            v = (u32x4){__float_as_uint(m), __float_as_uint(l), 0u, 0u};
+            v = (u32x4){__float_as_uint(rm_s[r]), __float_as_uint(rl_s[r]), 0u, 0u};
         } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 4 * (c4 - 1) + j;
-                v[j] = e < hd ? __float_as_uint(combine(r, e, m, l)) : 0u;
-            }
+            // hd is a multiple of 8, so every group of 4 values is inside the head
+            const float4 a = combine4(r, 4 * (c4 - 1));
+            v = (u32x4){__float_as_uint(a.x), __float_as_uint(a.y), __float_as_uint(a.z), __float_as_uint(a.w)};
         }
-        __builtin_amdgcn_raw_buffer_store_b128(v, prs, rec_off(r, split) + 16 * c4, 0, ATTN_MERGE_KERNEL ? 0 : SC1);
+        const int at = (int)(((((size_t)b * heads + kvh * group + r) * splits) + split) * (size_t)RS * 4) + 16 * c4;
+        __builtin_amdgcn_raw_buffer_store_b128(v, prs, at, 0, 0);
     }
-#if ATTN_MERGE_KERNEL
-    return;  // attention_decode_merge combines the records after this launch
-#endif
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every record store acknowledged before counting in
-    __syncthreads();
-    uint32_t *counter = counters + (size_t)b * kv_heads + kvh;
-    if (threadIdx.x == 0)
-        last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(used - 1);
-    __syncthreads();
-    if (!last_s) return;
-
     ATT_T(5);
-    // ---- 8. the last chunk to arrive merges every record of its rows
-    merge_records<BF16IO, R, NW>(prs, rec_off(0, 0), rec_off(1, 0) - rec_off(0, 0), RS * 4, hd, group, used, hm_s,
-                                 &hl_s[0][0], &wacc_s[0][0][0], out, (size_t)b * heads + kvh * group);
-    ATT_T(7);
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The chunk records of each (sequence, kv head) merged after attention_decode: a workgroup per (kv head, sequence).
@@ -1204,9 +1225,7 @@ static void launch_split_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int 
     }
 }
 
-#ifndef ATTN_DEC_BPC
-#define ATTN_DEC_BPC 1
-#endif
+constexpr int DEC_BLOCKS_PER_CU = 1;  // one-token attention workgroups per compute unit the chunking aims at
 
 template <int F, int LPP, bool BF16IO, int R, bool FUSE, int U>
 static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
@@ -1217,12 +1236,12 @@ static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int c
         hipExtLaunchKernelGGL(kern, grid, dim3(64 * DEC_NW), 0u, g->stream, t0, t1, 0u, a.q, a.fuse, a.tables,
                               a.table_stride, (int)a.table_len, (const uint8_t *)g->zero_row, a.ctx, a.geom,
                               (int)a.heads, (int)a.kv_heads, chunk, splits, scale, a.partials,
-                              (int)(a.partial_floats * 4), a.counters, a.out);
+                              (int)(a.partial_floats * 4), a.out);
     else
         kern<<<grid, dim3(64 * DEC_NW), 0, g->stream>>>(a.q, a.fuse, a.tables, a.table_stride, (int)a.table_len,
                                                         (const uint8_t *)g->zero_row, a.ctx, a.geom, (int)a.heads,
                                                         (int)a.kv_heads, chunk, splits, scale, a.partials,
-                                                        (int)(a.partial_floats * 4), a.counters, a.out);
+                                                        (int)(a.partial_floats * 4), a.out);
 }
 
 template <int F, int LPP, int R, int U>
@@ -1264,7 +1283,7 @@ static void launch_decode_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int
     }
 }
 
-// The one-token kernel's chunking for a context bound: about ATTN_DEC_BPC workgroups per compute unit in all (a
+// The one-token kernel's chunking for a context bound: about DEC_BLOCKS_PER_CU workgroups per compute unit in all (a
 // few workgroups past a whole number per unit would share units with others and set the launch's tail), chunks of
 // any length up to what the largest burst of loads covers. 0 when that needs more chunks
 // than the last workgroup merges.
@@ -1275,7 +1294,7 @@ static int decode_chunk(const AttentionArgs &a, int cu_count, int &splits) {
     const int umax = a.geom.format == MARIN_KV_F32 ? (r4 ? dec_umax<MARIN_KV_F32, 4>() : dec_umax<MARIN_KV_F32, 8>())
                                                    : (r4 ? dec_umax<MARIN_KV_F16, 4>() : dec_umax<MARIN_KV_F16, 8>());
     const size_t units = std::max<size_t>(a.kv_heads * a.batch, 1);
-    const size_t per_unit = std::max<size_t>(1, (size_t)ATTN_DEC_BPC * std::max(cu_count, 1) / units);
+    const size_t per_unit = std::max<size_t>(1, (size_t)DEC_BLOCKS_PER_CU * std::max(cu_count, 1) / units);
     size_t chunk = (a.max_ctx + per_unit - 1) / per_unit;
     chunk = std::min<size_t>(std::max<size_t>(chunk, (size_t)step), (size_t)umax * step);
     const size_t n = (a.max_ctx + chunk - 1) / chunk;
@@ -1314,7 +1333,6 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
         if (a.table_len == 0 || a.table_len > 0x7fffffffu) shape("decode attention page table entries", 1, a.table_len);
         if (a.geom.head_dim * kv_elem_bytes((marin_kv_format)a.geom.format) > 4096)
             unsupported("decode attention row bytes", 4096, a.geom.head_dim * kv_elem_bytes((marin_kv_format)a.geom.format));
-        if (a.batch * a.kv_heads > a.counter_count) shape("attention chunk counters", a.batch * a.kv_heads, a.counter_count);
         const size_t dneed = a.batch * a.heads * (size_t)dsplits * (size_t)rec_floats((int)a.geom.head_dim);
         if (dsplits > 1 && dneed > a.partial_floats) shape("attention partial records (floats)", dneed, a.partial_floats);
         if (a.partial_floats * 4 >= ((size_t)1 << 31))
@@ -1328,7 +1346,7 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
             }
             g->launched(marin_gpu::ATTENTION, a.bytes_hint, "attention_decode");
         }
-        if (ATTN_MERGE_KERNEL && dsplits > 1 && !(g->only && strcmp(g->only, "attention_decode_merge"))) {
+        if (dsplits > 1 && !(g->only && strcmp(g->only, "attention_decode_merge"))) {
             dim3 mgrid((unsigned)a.kv_heads, (unsigned)a.batch);
             const bool r4 = a.heads / a.kv_heads <= 4;
             const int pb = (int)(a.partial_floats * 4);
