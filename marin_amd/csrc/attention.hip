@@ -1114,26 +1114,26 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode(
     ATT_T(5);
 }
 
-// The chunk records of each (sequence, kv head) merged after attention_decode: a workgroup per (kv head, sequence).
-template <bool BF16IO, int R>
+// The chunk records of each (sequence, q head) merged after attention_decode: a workgroup per (q head, sequence),
+// so each workgroup reads one head's records (a few tens of KB) and the launch spreads over many compute units.
+template <bool BF16IO>
 __global__ __launch_bounds__(64 * DEC_NW) void attention_decode_merge(const float *__restrict__ part, int part_bytes,
                                                                       const uint32_t *__restrict__ ctx_lens, int hd,
-                                                                      int heads, int kv_heads, int chunk, int splits,
+                                                                      int heads, int chunk, int splits,
                                                                       void *__restrict__ out) {
-    __shared__ float wt_s[R][DEC_MAX_SPLITS];
-    __shared__ float lsum_s[R];
-    __shared__ float sh_s[3 * R * 256];
-    const int kvh = blockIdx.x, b = blockIdx.y;
-    const int group = heads / kv_heads;
+    __shared__ float wt_s[1][DEC_MAX_SPLITS];
+    __shared__ float lsum_s[1];
+    __shared__ float sh_s[3 * 256];
+    const int h = blockIdx.x, b = blockIdx.y;
     const int ctx = (int)ctx_lens[b];
     const int used = (ctx + chunk - 1) / chunk;
     if (used <= 1) return;  // a context of one chunk was written by attention_decode itself
     const int RS = rec_floats(hd);
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(part), (short)0, part_bytes,
                                                                        0x00020000);
-    const int rec0 = (int)(((size_t)b * heads + kvh * group) * splits * (size_t)RS * 4);
-    merge_records<BF16IO, R, DEC_NW>(prs, rec0, splits * RS * 4, RS * 4, hd, group, used, wt_s, lsum_s, sh_s, out,
-                                     (size_t)b * heads + kvh * group);
+    const int rec0 = (int)(((size_t)b * heads + h) * splits * (size_t)RS * 4);
+    merge_records<BF16IO, 1, DEC_NW>(prs, rec0, splits * RS * 4, RS * 4, hd, 1, used, wt_s, lsum_s, sh_s, out,
+                                     (size_t)b * heads + h);
 }
 
 #ifndef ATTN_NW
@@ -1347,17 +1347,13 @@ void launch_attention(marin_gpu *g, const AttentionArgs &a) {
             g->launched(marin_gpu::ATTENTION, a.bytes_hint, "attention_decode");
         }
         if (dsplits > 1 && !(g->only && strcmp(g->only, "attention_decode_merge"))) {
-            dim3 mgrid((unsigned)a.kv_heads, (unsigned)a.batch);
-            const bool r4 = a.heads / a.kv_heads <= 4;
+            dim3 mgrid((unsigned)a.heads, (unsigned)a.batch);
             const int pb = (int)(a.partial_floats * 4);
-            const int hd = (int)a.geom.head_dim, H = (int)a.heads, KV = (int)a.kv_heads;
-            if (a.bf16_io) {
-                if (r4) attention_decode_merge<true, 4><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
-                else attention_decode_merge<true, 8><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
-            } else {
-                if (r4) attention_decode_merge<false, 4><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
-                else attention_decode_merge<false, 8><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, KV, dchunk, dsplits, a.out);
-            }
+            const int hd = (int)a.geom.head_dim, H = (int)a.heads;
+            if (a.bf16_io)
+                attention_decode_merge<true><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, dchunk, dsplits, a.out);
+            else
+                attention_decode_merge<false><<<mgrid, 64 * DEC_NW, 0, g->stream>>>(a.partials, pb, a.ctx, hd, H, dchunk, dsplits, a.out);
             g->launched(marin_gpu::OTHER, 0.0, "attention_decode_merge");
         }
         return;
