@@ -178,6 +178,10 @@ __device__ __forceinline__ void norm_rope_head(const float *__restrict__ src, co
     finish_head(load_head(src, w, freq, hd, lane), pos, hd, eps, lane, a, b);
 }
 
+// Diagnostic build flag ATTN_TIMING (off in every shipped build; ATT_T then compiles to nothing): thread 0 of each
+// workgroup records the 100 MHz wall clock at numbered points of the attention kernels into attn_dbg, eight slots per
+// workgroup, read back by marin_attn_dbg. In attention_decode: 6 entry, 0 context length known, 1 row loads issued,
+// 2 query ready, 3 softmax done, 4 partials combined, 5 records written.
 #ifdef ATTN_TIMING
 __device__ unsigned long long attn_dbg[65536 * 8];
 #define ATT_T(k)                                                                                                 \
@@ -208,10 +212,7 @@ extern "C" void marin_attn_dbg_clear() {
 // FUSE: q and the new tokens' keys and values are the raw projections [tokens][heads + 2 kv_heads][hd]; the kernel
 // applies q/k RMSNorm and RoPE itself and stores the new keys and values of its chunk into the cache before reading
 // it (every row group of the chunk stores the same bytes).
-#ifndef ATTN_POS_IN_FLIGHT
-#define ATTN_POS_IN_FLIGHT 2
-#endif
-constexpr int POS_IN_FLIGHT = ATTN_POS_IN_FLIGHT;  // positions per lane group loaded together
+constexpr int POS_IN_FLIGHT = 2;  // positions per lane group loaded together
 constexpr int GROUP = 16;         // chunks merged together at the first level
 
 // Records: [max, sum, 0, 0, values, pad] of rec_floats(hd) floats (a multiple of 4), written and read with 16-byte
@@ -1136,14 +1137,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void attention_decode_merge(const floa
                                      (size_t)b * heads + h);
 }
 
-#ifndef ATTN_NW
-#define ATTN_NW 4
-#endif
-#ifndef ATTN_BPC
-#define ATTN_BPC 4
-#endif
-constexpr int NWAVES = ATTN_NW;          // waves per attention workgroup
-constexpr int BLOCKS_PER_CU = ATTN_BPC;  // workgroups the chunk size aims at per compute unit
+constexpr int NWAVES = 4;         // waves per attention workgroup
+constexpr int BLOCKS_PER_CU = 4;  // workgroups the chunk size aims at per compute unit
 
 // Positions per workgroup: about BLOCKS_PER_CU workgroups per compute unit, MIN_CHUNK to MAX_CHUNK positions each,
 // rounded up to what one step of the workgroup's lanes covers so no lane group idles.
