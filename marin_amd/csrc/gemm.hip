@@ -48,12 +48,15 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 // FRAG false: limbs [token][limb][column]. FRAG true (the batch product): the limbs already in B-operand order,
 // [window][token tile][64 lanes][16 bytes] with lane 16 q + 4 (token % 4) + limb holding columns 64 w + 16 q .. + 16,
 // so each B fragment is one contiguous KiB; `ttiles` = token tiles of 4.
-template <int GCOLS, bool FRAG>
+// L: limbs per value, 4 (30 bits below the group's largest magnitude) or 3 (22 bits, limbs [token][3][column],
+// FRAG false only).
+template <int GCOLS, bool FRAG, int L = 4>
 __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, int8_t *__restrict__ limbs,
                                                            float *__restrict__ exps, float *__restrict__ rs_out,
                                                            int ttiles) {
     constexpr int TPG = GCOLS / 4;  // threads per group, 4 consecutive columns each
     static_assert(TPG <= 64 && (TPG & (TPG - 1)) == 0, "group width");
+    static_assert(L == 4 || (L == 3 && !FRAG), "limbs");
     __shared__ float red[QA_THREADS / 64];
     const int t = blockIdx.x;
     const int groups = cols / GCOLS;
@@ -112,30 +115,30 @@ __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, 
         if (mx > 0.0f && mx < INFINITY) {
             int e;
             (void)frexpf(mx, &e);
-            sh = 30 - e;
+            sh = (8 * L - 2) - e;  // largest magnitude in [2^(8L-3), 2^(8L-2)): the top limb stays a signed byte
             sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
         }
         if (!on) continue;
         const float up = ldexpf(1.0f, sh);
-        uint32_t word[4] = {0u, 0u, 0u, 0u};
+        uint32_t word[L] = {};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             int xi = __float2int_rn(v[e] * up);
 #pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const int lb = l == 3 ? xi : (int)(int8_t)(xi & 0xff);
+            for (int l = 0; l < L; ++l) {
+                const int lb = l == L - 1 ? xi : (int)(int8_t)(xi & 0xff);
                 word[l] |= ((uint32_t)lb & 0xffu) << (8 * e);
                 xi = (xi - lb) >> 8;
             }
         }
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
+        for (int l = 0; l < L; ++l) {
             size_t at;
             if constexpr (FRAG) {
                 const int lane = ((k & 63) >> 4) * 16 + (t & 3) * 4 + l;
                 at = (((size_t)(k >> 6) * ttiles + (t >> 2)) * 64 + lane) * 16 + (k & 15);
             } else {
-                at = ((size_t)t * 4 + l) * cols + k;
+                at = ((size_t)t * L + l) * cols + k;
             }
             *reinterpret_cast<uint32_t *>(limbs + at) = word[l];
         }
@@ -478,6 +481,243 @@ __global__ __launch_bounds__(64 * GM_WAVES * gm_halves(TOK)) void gemm_q8(const 
     }
 }
 
+// The prompt GEMM (gemm_prompt): prompt passes of GP_MIN_TOKENS+ tokens, a redesign of gemm_q8 around the
+// matrix cores' feed. Activations are 22-bit fixed point below each (token, group)'s largest magnitude in three
+// signed 8-bit limbs (the arithmetic of the reference's integer path, mma.cu:160-268), stored [token][3][column].
+// A B operand holds 16 tokens of one limb (limb-major), so a 16x16x64 MFMA does a third more useful work than four
+// limbs of 4 tokens. A workgroup of GP_WM x GP_WN waves computes GP_ROWS rows x GP_TOK tokens; a wave owns GP_RT
+// 16-row tiles x GP_TN 16-token tiles, so every A fragment it reads from LDS feeds 6 MFMAs and every B fragment 4.
+//
+// Each 64-column window's operands (the rows' code windows, the tokens' limb fragments, the group's weight scales
+// and token factors) go from memory straight into LDS (global_load_lds, 16 bytes a lane, no registers), into one of
+// GP_STAGES stages, GP_STAGES - 1 windows ahead of the window being computed. Every wave issues the same number of
+// these loads per window, so one counted wait (vmcnt) plus one barrier per window proves the window's stage complete
+// for all waves and the previous stage free. The main loop issues no other vector-memory instruction, so the counts
+// are exact.
+//
+// Workgroups are numbered so that all token blocks of a row block fall on one XCD (workgroup i runs on XCD i % 8):
+// the row block's codes come from HBM once into that XCD's L2 and serve all of them.
+constexpr int GP_WM = 4, GP_WN = 2, GP_RT = 4, GP_TN = 2, GP_L = 3;
+constexpr int GP_ROWS = GP_WM * GP_RT * 16;  // rows per workgroup
+constexpr int GP_TILES = GP_ROWS / 16;
+constexpr int GP_TOK = GP_WN * GP_TN * 16;   // tokens per workgroup
+constexpr int GP_WAVES = GP_WM * GP_WN;
+constexpr int GP_THREADS = 64 * GP_WAVES;
+constexpr int GP_STAGES = 4;
+constexpr size_t GP_MIN_TOKENS = 32;
+// One stage: A [tile][64 lanes][16 B] | B [token tile][limb][64 lanes][16 B] | scales [rows] f32 (bf16: the first
+// half) | token factors [tokens] f32 | pad (the spare loads' target)
+constexpr int GP_A_BYTES = GP_TILES * 1024, GP_B_BYTES = GP_WN * GP_TN * GP_L * 1024;
+constexpr int GP_SC_OFF = GP_A_BYTES + GP_B_BYTES, GP_EX_OFF = GP_SC_OFF + GP_ROWS * 4, GP_PAD_OFF = GP_EX_OFF + GP_TOK * 4;
+constexpr int GP_STAGE_BYTES = (GP_PAD_OFF + 1024 + 255) / 256 * 256;
+// loads per window: A tiles, B fragments, scales, token factors; padded to a whole number per wave
+constexpr int GP_LOADS = GP_TILES + GP_WN * GP_TN * GP_L + 2;
+constexpr int GP_LPW = (GP_LOADS + GP_WAVES - 1) / GP_WAVES;
+static_assert(GP_TOK <= 64, "one token factor per lane");
+
+typedef __attribute__((address_space(3))) void gp_lds_t;
+typedef __attribute__((address_space(1))) const void gp_glb_t;
+
+template <int WG, typename ST>
+__global__ __launch_bounds__(GP_THREADS, 1) void gemm_prompt(const uint8_t *__restrict__ codes,
+                                                              const ST *__restrict__ scales,
+                                                              const int8_t *__restrict__ limbs,
+                                                              const float *__restrict__ exps,
+                                                              const float *__restrict__ rsv, GemvOut out, int tokens,
+                                                              int rows, int cols, int tiles, int row_blocks,
+                                                              int token_blocks) {
+    extern __shared__ __align__(256) unsigned char gp_lds[];
+    // XCD-aware numbering: ids in runs of 8 x token_blocks; within a run, id % 8 picks the row block, id / 8 the
+    // token block
+    const int run = 8 * token_blocks, id = (int)blockIdx.x;
+    const int rb = (id / run) * 8 + id % 8, tb = (id % run) / 8;
+    if (rb >= row_blocks) return;  // the whole workgroup, before any barrier
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave % GP_WM, wn = wave / GP_WM;
+    const int c = lane & 15, q = lane >> 4;
+    const int windows = cols >> 6;
+    const int groups = windows / WG;
+    const int t0 = tb * GP_TOK;
+    const int tbase = rb * GP_TILES;
+    const size_t tile_bytes = (size_t)16 * cols;
+
+    // the wave's loads of window `win` into stage `st` (a window past the last loads the last one again)
+    auto issue = [&](int win, int st) {
+        win = min(win, windows - 1);
+        const int g = win / WG;
+        unsigned char *base = gp_lds + st * GP_STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < GP_LPW; ++i) {
+            const int k = wave * GP_LPW + i;  // wave-uniform
+            if (k < GP_TILES) {
+                const int tl = min(tbase + k, tiles - 1);
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(codes + (size_t)tl * tile_bytes + (size_t)win * 1024 + 16 * lane),
+                                                 (gp_lds_t *)(base + k * 1024), 16, 0, 0);
+            } else if (k < GP_TILES + GP_WN * GP_TN * GP_L) {
+                const int f = k - GP_TILES, j = f / GP_L, l = f % GP_L;
+                const int tok = min(t0 + 16 * j + c, tokens - 1);
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(limbs + ((size_t)tok * GP_L + l) * cols + 64 * win + 16 * q),
+                                                 (gp_lds_t *)(base + GP_A_BYTES + f * 1024), 16, 0, 0);
+            } else if (k == GP_TILES + GP_WN * GP_TN * GP_L) {
+                // 16 bytes a lane: f32 scales of 4 rows (lane l: tile l / 4), bf16 of 8 rows (lanes 32+ repeat)
+                const int r0 = sizeof(ST) == 4 ? 4 * lane : 8 * (lane & 31);
+                const int tl = min(tbase + r0 / 16, tiles - 1);
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(scales + ((size_t)tl * groups + g) * 16 + r0 % 16),
+                                                 (gp_lds_t *)(base + GP_SC_OFF), 16, 0, 0);
+            } else if (k == GP_TILES + GP_WN * GP_TN * GP_L + 1) {
+                const int tok = min(t0 + lane, tokens - 1);
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(exps + (size_t)tok * groups + g),
+                                                 (gp_lds_t *)(base + GP_EX_OFF), 4, 0, 0);
+            } else {
+                // spare load: keeps every wave's count per window equal
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(exps + (size_t)min(t0 + lane, tokens - 1) * groups + g),
+                                                 (gp_lds_t *)(base + GP_PAD_OFF), 4, 0, 0);
+            }
+        }
+    };
+
+    floatx4 total[GP_RT][GP_TN];
+#pragma unroll
+    for (int rt = 0; rt < GP_RT; ++rt)
+#pragma unroll
+        for (int j = 0; j < GP_TN; ++j) total[rt][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+
+    // One group: per window (from its stage) the MFMAs into int32 sums over the group (each below 2^21 in
+    // magnitude), then the limbs recombined once: l0 + 256 l1 in an integer (below 2^30), + 65536 l2 in f32, scaled
+    // by weight scale x the token's 2^-s.
+    int4v acc[GP_RT][GP_TN][GP_L];
+    auto mfmas = [&](int st) {
+        const unsigned char *base = gp_lds + st * GP_STAGE_BYTES;
+        int4v af[GP_RT];
+#pragma unroll
+        for (int rt = 0; rt < GP_RT; ++rt)
+            af[rt] = *reinterpret_cast<const int4v *>(base + (wm * GP_RT + rt) * 1024 + 16 * lane);
+#pragma unroll
+        for (int j = 0; j < GP_TN; ++j) {
+#pragma unroll
+            for (int l = 0; l < GP_L; ++l) {
+                const int4v bfrag = *reinterpret_cast<const int4v *>(base + GP_A_BYTES + ((wn * GP_TN + j) * GP_L + l) * 1024 + 16 * lane);
+#pragma unroll
+                for (int rt = 0; rt < GP_RT; ++rt)
+                    acc[rt][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rt], bfrag, acc[rt][j][l], 0, 0, 0);
+            }
+        }
+    };
+    auto finish = [&](int st) {
+        const unsigned char *base = gp_lds + st * GP_STAGE_BYTES;
+        // lane (q, c): rows 4q..4q+3 of each tile, token 16 (wn GP_TN + j) + c
+        floatx4 sc[GP_RT];
+#pragma unroll
+        for (int rt = 0; rt < GP_RT; ++rt) {
+            const int r = (wm * GP_RT + rt) * 16 + 4 * q;
+            if constexpr (sizeof(ST) == 4) {
+                sc[rt] = *reinterpret_cast<const floatx4 *>(base + GP_SC_OFF + 4 * r);
+            } else {
+                const uint2 sv = *reinterpret_cast<const uint2 *>(base + GP_SC_OFF + 2 * r);
+                sc[rt] = (floatx4){__uint_as_float(sv.x << 16), __uint_as_float(sv.x & 0xffff0000u),
+                                   __uint_as_float(sv.y << 16), __uint_as_float(sv.y & 0xffff0000u)};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < GP_TN; ++j) {
+            const float tf = *reinterpret_cast<const float *>(base + GP_EX_OFF + 4 * (16 * (wn * GP_TN + j) + c));
+#pragma unroll
+            for (int rt = 0; rt < GP_RT; ++rt) {
+                const floatx4 m = sc[rt] * tf;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int lo = acc[rt][j][0][k] + (acc[rt][j][1][k] << 8);
+                    total[rt][j][k] += ((float)lo + 65536.0f * (float)acc[rt][j][2][k]) * m[k];
+                }
+            }
+        }
+    };
+
+    // windows 0 .. GP_STAGES - 2 in flight, then per window: wait for this window's loads (the later windows' may
+    // stay in flight), meet the other waves (the window is complete for all, and the stage computed last is free),
+    // issue the window GP_STAGES - 1 ahead into that stage, compute.
+#pragma unroll
+    for (int i = 0; i < GP_STAGES - 1; ++i) issue(i, i);
+    for (int g = 0; g < groups; ++g) {
+#pragma unroll
+        for (int rt = 0; rt < GP_RT; ++rt)
+#pragma unroll
+            for (int j = 0; j < GP_TN; ++j)
+#pragma unroll
+                for (int l = 0; l < GP_L; ++l) acc[rt][j][l] = (int4v){0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < WG; ++w) {
+            const int i = g * WG + w;
+            // at most the loads of windows i + 1 .. i + GP_STAGES - 2 outstanding
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((GP_STAGES - 2) * GP_LPW) : "memory");
+            __builtin_amdgcn_s_barrier();
+            issue(i + GP_STAGES - 1, (i + GP_STAGES - 1) % GP_STAGES);
+            mfmas(i % GP_STAGES);
+            if (w == WG - 1) finish(i % GP_STAGES);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the spare loads past the last window land before exit
+    __builtin_amdgcn_s_barrier();
+
+    const int tile0 = tbase + wm * GP_RT;
+#pragma unroll
+    for (int rt = 0; rt < GP_RT; ++rt) {
+        const int tile = tile0 + rt;
+        const int row0 = tile * 16 + 4 * q;
+#pragma unroll
+        for (int j = 0; j < GP_TN; ++j) {
+            const int tok = t0 + 16 * (wn * GP_TN + j) + c;
+            if (tok >= tokens || tile >= tiles) continue;
+            const float r = rsv[tok];
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = total[rt][j][k] * r;
+            if (out.mode == OUT_SILU) {
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) {
+                    const int row = row0 + k;
+                    if (row < rows)
+                        reinterpret_cast<float *>(out.y)[(size_t)tok * out.y_stride + (row >> 1)] = silu_f(v[k]) * v[k + 1];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int row = row0 + k;
+                    if (row >= rows) continue;
+                    const size_t at = (size_t)tok * out.y_stride + row;
+                    if (out.mode == OUT_F32) reinterpret_cast<float *>(out.y)[at] = v[k];
+                    else if (out.mode == OUT_ADD) reinterpret_cast<float *>(out.y)[at] += v[k];
+                    else {
+                        const unsigned uu = __float_as_uint(v[k]);
+                        reinterpret_cast<uint16_t *>(out.y)[at] = (uint16_t)(
+                            (uu & 0x7fffffffu) > 0x7f800000u ? (uu >> 16) | 0x40u
+                                                             : (uu + 0x7fffu + ((uu >> 16) & 1u)) >> 16);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int WG, typename ST>
+static void launch_prompt_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
+                            const float *rs, const GemvOut &out, size_t tokens) {
+    const int tiles = (int)(w->rows_padded / 16);
+    const int row_blocks = (int)((w->rows_padded + GP_ROWS - 1) / GP_ROWS);
+    const int token_blocks = (int)((tokens + GP_TOK - 1) / GP_TOK);
+    const unsigned grid = (unsigned)((row_blocks + 7) / 8 * 8 * token_blocks);
+    const size_t lds = (size_t)GP_STAGES * GP_STAGE_BYTES;
+    static bool attr = false;  // dynamic LDS above 64 KiB must be allowed once per kernel
+    if (!attr) {
+        HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    gemm_prompt<WG, ST><<<grid, GP_THREADS, lds, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
+                                                             (int)tokens, (int)w->rows, (int)w->cols, tiles,
+                                                             row_blocks, token_blocks);
+}
+
 bool gemm_layout_ok(const marin_quant_matrix *w) {
     return w->bits == 8 && w->windowed && (w->group == 64 || w->group == 128) && w->cols % w->group == 0;
 }
@@ -511,17 +751,31 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     if (!gemm_layout_ok(w)) unsupported("matrix-core GEMM layout (int8, group 64 or 128)", 128, w->group);
     if (out.argmax && !out.argmax_each) unsupported("GEMM greedy choice (one per token only)", 1, 0);
     const size_t cols = w->cols, groups = w->groups();
-    // workspace: limbs [tokens][4][cols] | exps [tokens][groups] | rs [tokens]
-    const size_t limb_bytes = (tokens * 4 * cols + 15) / 16 * 16;
+    const bool prompt = tokens >= GP_MIN_TOKENS && !out.argmax;
+    const int nl = prompt ? GP_L : 4;
+    // workspace: limbs [tokens][nl][cols] | exps [tokens][groups] | rs [tokens]
+    const size_t limb_bytes = (tokens * nl * cols + 15) / 16 * 16;
     const size_t exp_bytes = (tokens * groups * 4 + 15) / 16 * 16;
     uint8_t *ws = (uint8_t *)g->workspace(limb_bytes + exp_bytes + tokens * 4);
     int8_t *limbs = (int8_t *)ws;
     float *exps = (float *)(ws + limb_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
+    const bool wg2 = w->group == 128;
+    if (prompt) {
+        if (wg2) quantize_act<128, false, GP_L><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+        else quantize_act<64, false, GP_L><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+        g->launched();
+        if (w->bf16_scales) {
+            if (wg2) launch_prompt_t<2, uint16_t>(g, w, limbs, exps, rs, out, tokens);
+            else launch_prompt_t<1, uint16_t>(g, w, limbs, exps, rs, out, tokens);
+        } else {
+            if (wg2) launch_prompt_t<2, float>(g, w, limbs, exps, rs, out, tokens);
+            else launch_prompt_t<1, float>(g, w, limbs, exps, rs, out, tokens);
+        }
+    } else {
     if (w->group == 128) quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
     else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
     g->launched();
-    const bool wg2 = w->group == 128;
     if (w->bf16_scales) {
         if (wg2) launch_t<2, uint16_t>(g, w, limbs, exps, rs, out, tokens);
         else launch_t<1, uint16_t>(g, w, limbs, exps, rs, out, tokens);
@@ -529,11 +783,12 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
         if (wg2) launch_t<2, float>(g, w, limbs, exps, rs, out, tokens);
         else launch_t<1, float>(g, w, limbs, exps, rs, out, tokens);
     }
+    }
     const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;
     const double outs = out.mode == OUT_SILU ? (double)w->rows / 2 : (double)w->rows;
     const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * groups * (w->bf16_scales ? 2 : 4) +
                          (double)tokens * cols * act + (double)tokens * outs * res;
-    g->launched(marin_gpu::GEMV, bytes, "gemm_q8");
+    g->launched(marin_gpu::GEMV, bytes, prompt ? "gemm_prompt" : "gemm_q8");
 }
 
 static size_t align16(size_t n) { return (n + 15) / 16 * 16; }
