@@ -542,6 +542,38 @@ __global__ __launch_bounds__(GP_THREADS, 1) void gemm_prompt(const uint8_t *__re
     const int tbase = rb * GP_TILES;
     const size_t tile_bytes = (size_t)16 * cols;
 
+    // The wave's GP_LPW loads per window: each slot's per-lane source address without the window's offset, worked
+    // out once (the loop adds a wave-uniform offset), its kind and its LDS offset inside a stage.
+    const unsigned char *src[GP_LPW];
+    int kind[GP_LPW], dst[GP_LPW];
+#pragma unroll
+    for (int i = 0; i < GP_LPW; ++i) {
+        const int k = wave * GP_LPW + i;  // wave-uniform
+        if (k < GP_TILES) {
+            const int tl = min(tbase + k, tiles - 1);
+            src[i] = codes + (size_t)tl * tile_bytes + 16 * lane;
+            kind[i] = 0;
+            dst[i] = k * 1024;
+        } else if (k < GP_TILES + GP_WN * GP_TN * GP_L) {
+            const int f = k - GP_TILES, j = f / GP_L, l = f % GP_L;
+            const int tok = min(t0 + 16 * j + c, tokens - 1);
+            src[i] = reinterpret_cast<const unsigned char *>(limbs + ((size_t)tok * GP_L + l) * cols + 16 * q);
+            kind[i] = 1;
+            dst[i] = GP_A_BYTES + f * 1024;
+        } else if (k == GP_TILES + GP_WN * GP_TN * GP_L) {
+            // 16 bytes a lane: f32 scales of 4 rows (lane l: tile l / 4), bf16 of 8 rows (lanes 32+ repeat)
+            const int r0 = sizeof(ST) == 4 ? 4 * lane : 8 * (lane & 31);
+            const int tl = min(tbase + r0 / 16, tiles - 1);
+            src[i] = reinterpret_cast<const unsigned char *>(scales + (size_t)tl * groups * 16 + r0 % 16);
+            kind[i] = 2;
+            dst[i] = GP_SC_OFF;
+        } else {
+            // the token factors (4 bytes a lane); past them, spare loads that keep every wave's count equal
+            src[i] = reinterpret_cast<const unsigned char *>(exps + (size_t)min(t0 + lane, tokens - 1) * groups);
+            kind[i] = 3;
+            dst[i] = k == GP_TILES + GP_WN * GP_TN * GP_L + 1 ? GP_EX_OFF : GP_PAD_OFF;
+        }
+    }
     // the wave's loads of window `win` into stage `st` (a window past the last loads the last one again)
     auto issue = [&](int win, int st) {
         win = min(win, windows - 1);
@@ -549,31 +581,14 @@ __global__ __launch_bounds__(GP_THREADS, 1) void gemm_prompt(const uint8_t *__re
         unsigned char *base = gp_lds + st * GP_STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < GP_LPW; ++i) {
-            const int k = wave * GP_LPW + i;  // wave-uniform
-            if (k < GP_TILES) {
-                const int tl = min(tbase + k, tiles - 1);
-                __builtin_amdgcn_global_load_lds((gp_glb_t *)(codes + (size_t)tl * tile_bytes + (size_t)win * 1024 + 16 * lane),
-                                                 (gp_lds_t *)(base + k * 1024), 16, 0, 0);
-            } else if (k < GP_TILES + GP_WN * GP_TN * GP_L) {
-                const int f = k - GP_TILES, j = f / GP_L, l = f % GP_L;
-                const int tok = min(t0 + 16 * j + c, tokens - 1);
-                __builtin_amdgcn_global_load_lds((gp_glb_t *)(limbs + ((size_t)tok * GP_L + l) * cols + 64 * win + 16 * q),
-                                                 (gp_lds_t *)(base + GP_A_BYTES + f * 1024), 16, 0, 0);
-            } else if (k == GP_TILES + GP_WN * GP_TN * GP_L) {
-                // 16 bytes a lane: f32 scales of 4 rows (lane l: tile l / 4), bf16 of 8 rows (lanes 32+ repeat)
-                const int r0 = sizeof(ST) == 4 ? 4 * lane : 8 * (lane & 31);
-                const int tl = min(tbase + r0 / 16, tiles - 1);
-                __builtin_amdgcn_global_load_lds((gp_glb_t *)(scales + ((size_t)tl * groups + g) * 16 + r0 % 16),
-                                                 (gp_lds_t *)(base + GP_SC_OFF), 16, 0, 0);
-            } else if (k == GP_TILES + GP_WN * GP_TN * GP_L + 1) {
-                const int tok = min(t0 + lane, tokens - 1);
-                __builtin_amdgcn_global_load_lds((gp_glb_t *)(exps + (size_t)tok * groups + g),
-                                                 (gp_lds_t *)(base + GP_EX_OFF), 4, 0, 0);
-            } else {
-                // spare load: keeps every wave's count per window equal
-                __builtin_amdgcn_global_load_lds((gp_glb_t *)(exps + (size_t)min(t0 + lane, tokens - 1) * groups + g),
-                                                 (gp_lds_t *)(base + GP_PAD_OFF), 4, 0, 0);
-            }
+            if (kind[i] == 0)
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(src[i] + (size_t)win * 1024), (gp_lds_t *)(base + dst[i]), 16, 0, 0);
+            else if (kind[i] == 1)
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(src[i] + 64 * win), (gp_lds_t *)(base + dst[i]), 16, 0, 0);
+            else if (kind[i] == 2)
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(src[i] + (size_t)g * 16 * sizeof(ST)), (gp_lds_t *)(base + dst[i]), 16, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds((gp_glb_t *)(src[i] + (size_t)g * 4), (gp_lds_t *)(base + dst[i]), 4, 0, 0);
         }
     };
 
