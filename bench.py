@@ -29,6 +29,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
 
 
@@ -345,6 +346,64 @@ def bench_linear(m, args) -> int:
     return 0
 
 
+def bench_prefill(m, args) -> int:
+    """The prompt GEMM alone (prefill's products): each 8B projection shape times 512 tokens (one prompt chunk), f32
+    activations N(0, 1) and f32 out, weights N(0, 0.02) quantized int8 g128 on the device; `reps` eager products
+    between two events (each with its activation-limb pass). Useful work 2 N K T int8 operations per product; the
+    matrix cores execute 3 limbs of it (the activations' 22-bit fixed point). value: useful int8 TOP/s over the four
+    shapes."""
+    gpu = m.Gpu()
+    rng = np.random.default_rng(args.seed)
+    T = 512
+    shapes = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576), ("down", 12288, 4096)]
+    cases, tot_ops, tot_s = [], 0.0, 0.0
+    for name, K, N in shapes:
+        w = gpu.quantized_synthetic(N, K, 128, args.seed, 0)
+        x = gpu.upload(rng.standard_normal(T * K).astype(np.float32))
+        out = gpu.zeros(T * N)
+        for _ in range(3):
+            gpu.matmul_quant(w, x, T, out)
+        gpu.synchronize()
+        if args.counters:
+            counter_marker(gpu)
+            gpu.matmul_quant(w, x, T, out)
+            counter_marker(gpu)
+            del w
+            continue
+        reps = 20
+        a = gpu.mark()
+        for _ in range(reps):
+            gpu.matmul_quant(w, x, T, out)
+        sec = gpu.mark().since(a) / reps
+        ops = 2.0 * N * K * T
+        tot_ops += ops
+        tot_s += sec
+        cases.append({"matrix": name, "K": K, "N": N, "tokens": T, "us": round(sec * 1e6, 1),
+                      "useful_int8_TOPs": round(ops / sec / 1e12, 1),
+                      "mfma_frac": round(3 * ops / sec / 1e12 / INT8_PEAK_TOPS, 4)})
+        print(f"[bench] prefill product {name} {N}x{K} x {T} tokens: {sec * 1e6:.1f} us, {ops / sec / 1e12:.0f} useful "
+              f"int8 TOP/s", file=sys.stderr, flush=True)
+        del w
+        gpu.synchronize()
+    if args.counters:
+        print(json.dumps({"counters": "prefill", "order": [c[0] for c in shapes]}))
+        return 0
+    tops = tot_ops / tot_s / 1e12
+    line = {
+        "metric": "prompt GEMM useful int8 TOP/s (Qwen3-8B projection shapes, 512-token chunk)", "value": round(tops, 1),
+        "unit": "TOP/s", "n_gpus": 1, "steps": 20, "warmup": 3, "ms_per_step": round(tot_s / len(shapes) * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (N(0,0.02) weights quantized int8 g128 on device; N(0,1) f32 activations)",
+        "config": {"workload": "prefill products: qkv, o, gate_up, down of Qwen3-8B at 512 tokens, f32 in and out"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_prompt (+ its quantize_act pass)", "achieved": round(3 * tops, 1),
+                     "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(3 * tops / INT8_PEAK_TOPS, 4),
+                     "traffic": None, "note": "achieved counts the three limbs the matrix cores execute"},
+        "cases": cases,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def bench_paged(m, args) -> int:
     """Config 2: batched paged GQA decode attention. Batch 16, 32 q / 8 kv heads, head_dim 128, bf16 q/k/v N(0,1),
     pages of 16 positions; contexts uniform in [512, 8192] (seeded); one pool of exactly the pages needed, dealt to
@@ -439,6 +498,9 @@ def main() -> int:
     ap.add_argument("--moe", action="store_true",
                     help="config 4 instead: the Qwen3-30B-A3B-shaped expert FFN stack at batch 1 and 8 (grouped-expert "
                          "GEMV GB/s), one JSON line")
+    ap.add_argument("--prefill", action="store_true",
+                    help="the prompt GEMM alone at the 8B projection shapes x 512 tokens (useful int8 TOP/s); one JSON "
+                         "line")
     ap.add_argument("--counters", action="store_true",
                     help="for rocprofv3 --pmc runs: set the mode's inputs up, then launch its measured work once, "
                          "eagerly, between two copy-probe markers, and exit (no timing, no JSON result line)")
@@ -468,6 +530,8 @@ def main() -> int:
         return bench_linear(m, args)
     if args.paged:
         return bench_paged(m, args)
+    if args.prefill:
+        return bench_prefill(m, args)
     if args.batch > 1:
         return bench_batch(m, args)
 

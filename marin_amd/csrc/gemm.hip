@@ -497,29 +497,32 @@ __global__ __launch_bounds__(64 * GM_WAVES * gm_halves(TOK)) void gemm_q8(const 
 //
 // Workgroups are numbered so that all token blocks of a row block fall on one XCD (workgroup i runs on XCD i % 8):
 // the row block's codes come from HBM once into that XCD's L2 and serve all of them.
-constexpr int GP_WM = 4, GP_WN = 2, GP_RT = 4, GP_TN = 2, GP_L = 3;
-constexpr int GP_ROWS = GP_WM * GP_RT * 16;  // rows per workgroup
-constexpr int GP_TILES = GP_ROWS / 16;
-constexpr int GP_TOK = GP_WN * GP_TN * 16;   // tokens per workgroup
-constexpr int GP_WAVES = GP_WM * GP_WN;
-constexpr int GP_THREADS = 64 * GP_WAVES;
-constexpr int GP_STAGES = 4;
+constexpr int GP_WN = 2, GP_RT = 4, GP_TN = 2, GP_L = 3;
+constexpr int GP_TOK = GP_WN * GP_TN * 16;  // tokens per workgroup
 constexpr size_t GP_MIN_TOKENS = 32;
-// One stage: A [tile][64 lanes][16 B] | B [token tile][limb][64 lanes][16 B] | scales [rows] f32 (bf16: the first
-// half) | token factors [tokens] f32 | pad (the spare loads' target)
-constexpr int GP_A_BYTES = GP_TILES * 1024, GP_B_BYTES = GP_WN * GP_TN * GP_L * 1024;
-constexpr int GP_SC_OFF = GP_A_BYTES + GP_B_BYTES, GP_EX_OFF = GP_SC_OFF + GP_ROWS * 4, GP_PAD_OFF = GP_EX_OFF + GP_TOK * 4;
-constexpr int GP_STAGE_BYTES = (GP_PAD_OFF + 1024 + 255) / 256 * 256;
-// loads per window: A tiles, B fragments, scales, token factors; padded to a whole number per wave
-constexpr int GP_LOADS = GP_TILES + GP_WN * GP_TN * GP_L + 2;
-constexpr int GP_LPW = (GP_LOADS + GP_WAVES - 1) / GP_WAVES;
 static_assert(GP_TOK <= 64, "one token factor per lane");
+// The workgroup's shape for GP_WM row waves (4: 256 rows; 2: 128 rows, for matrices whose 256-row blocks would leave
+// compute units idle) and its stage layout: A [tile][64 lanes][16 B] | B [token tile][limb][64 lanes][16 B] |
+// scales [rows] f32 (bf16: the first half) | token factors [tokens] f32 | pad (the spare loads' target)
+template <int WM>
+struct GpShape {
+    static constexpr int ROWS = WM * GP_RT * 16, TILES = ROWS / 16;
+    static constexpr int WAVES = WM * GP_WN, THREADS = 64 * WAVES;
+    static constexpr int STAGES = WM == 4 ? 4 : 3;  // 128-row workgroups: 3 stages, so two fit a compute unit
+    static constexpr int A_BYTES = TILES * 1024, B_BYTES = GP_WN * GP_TN * GP_L * 1024;
+    static constexpr int SC_OFF = A_BYTES + B_BYTES, EX_OFF = SC_OFF + 1024, PAD_OFF = EX_OFF + GP_TOK * 4;
+    static constexpr int STAGE_BYTES = (PAD_OFF + 1024 + 255) / 256 * 256;
+    // loads per window: A tiles, B fragments, scales, token factors; padded to a whole number per wave
+    static constexpr int LOADS = TILES + GP_WN * GP_TN * GP_L + 2;
+    static constexpr int LPW = (LOADS + WAVES - 1) / WAVES;
+    static_assert(ROWS * 4 <= 1024, "scales of one stage");
+};
 
 typedef __attribute__((address_space(3))) void gp_lds_t;
 typedef __attribute__((address_space(1))) const void gp_glb_t;
 
-template <int WG, typename ST>
-__global__ __launch_bounds__(GP_THREADS, 1) void gemm_prompt(const uint8_t *__restrict__ codes,
+template <int WG, typename ST, int WM>
+__global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_prompt(const uint8_t *__restrict__ codes,
                                                               const ST *__restrict__ scales,
                                                               const int8_t *__restrict__ limbs,
                                                               const float *__restrict__ exps,
@@ -527,6 +530,10 @@ __global__ __launch_bounds__(GP_THREADS, 1) void gemm_prompt(const uint8_t *__re
                                                               int rows, int cols, int tiles, int row_blocks,
                                                               int token_blocks) {
     extern __shared__ __align__(256) unsigned char gp_lds[];
+    using S = GpShape<WM>;
+    constexpr int GP_WM = WM, GP_TILES = S::TILES, GP_WAVES = S::WAVES, GP_LPW = S::LPW;
+    constexpr int GP_A_BYTES = S::A_BYTES, GP_SC_OFF = S::SC_OFF, GP_EX_OFF = S::EX_OFF, GP_PAD_OFF = S::PAD_OFF;
+    constexpr int GP_STAGE_BYTES = S::STAGE_BYTES, GP_STAGES = S::STAGES;
     // XCD-aware numbering: ids in runs of 8 x token_blocks; within a run, id % 8 picks the row block, id / 8 the
     // token block
     const int run = 8 * token_blocks, id = (int)blockIdx.x;
@@ -715,22 +722,33 @@ __global__ __launch_bounds__(GP_THREADS, 1) void gemm_prompt(const uint8_t *__re
     }
 }
 
+template <int WG, typename ST, int WM>
+static void launch_prompt_wm(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
+                             const float *rs, const GemvOut &out, size_t tokens) {
+    using S = GpShape<WM>;
+    const int tiles = (int)(w->rows_padded / 16);
+    const int row_blocks = (int)((w->rows_padded + S::ROWS - 1) / S::ROWS);
+    const int token_blocks = (int)((tokens + GP_TOK - 1) / GP_TOK);
+    const unsigned grid = (unsigned)((row_blocks + 7) / 8 * 8 * token_blocks);
+    const size_t lds = (size_t)S::STAGES * S::STAGE_BYTES;
+    static bool attr = false;  // dynamic LDS above 64 KiB must be allowed once per kernel
+    if (!attr) {
+        HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST, WM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    gemm_prompt<WG, ST, WM><<<grid, S::THREADS, lds, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
+                                                                   (int)tokens, (int)w->rows, (int)w->cols, tiles,
+                                                                   row_blocks, token_blocks);
+}
+
+// 256-row workgroups unless they would cover at most half the compute units, then 128-row ones (two fit a unit)
 template <int WG, typename ST>
 static void launch_prompt_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
                             const float *rs, const GemvOut &out, size_t tokens) {
-    const int tiles = (int)(w->rows_padded / 16);
-    const int row_blocks = (int)((w->rows_padded + GP_ROWS - 1) / GP_ROWS);
-    const int token_blocks = (int)((tokens + GP_TOK - 1) / GP_TOK);
-    const unsigned grid = (unsigned)((row_blocks + 7) / 8 * 8 * token_blocks);
-    const size_t lds = (size_t)GP_STAGES * GP_STAGE_BYTES;
-    static bool attr = false;  // dynamic LDS above 64 KiB must be allowed once per kernel
-    if (!attr) {
-        HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
-    gemm_prompt<WG, ST><<<grid, GP_THREADS, lds, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
-                                                             (int)tokens, (int)w->rows, (int)w->cols, tiles,
-                                                             row_blocks, token_blocks);
+    const size_t token_blocks = (tokens + GP_TOK - 1) / GP_TOK;
+    const size_t big = (w->rows_padded + GpShape<4>::ROWS - 1) / GpShape<4>::ROWS * token_blocks;
+    if (2 * big > (size_t)std::max(g->cu_count, 1)) launch_prompt_wm<WG, ST, 4>(g, w, limbs, exps, rs, out, tokens);
+    else launch_prompt_wm<WG, ST, 2>(g, w, limbs, exps, rs, out, tokens);
 }
 
 bool gemm_layout_ok(const marin_quant_matrix *w) {
