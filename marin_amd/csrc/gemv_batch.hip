@@ -57,12 +57,17 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 
 // BITS: 8 or 4 (nibbles stored as code + 8, unpacked to bytes; 8 x the group's limb sums come off the int32 sums);
 // WG: windows per quantization group; TT: token tiles of 4 (1 or 2); SM: windows per wave per tile; ST: scale type.
-template <int BITS, int WG, int TT, int SM, typename ST>
+// FUSE (int8, B fragments in registers): no separate limb pass; every wave builds the limbs of its own column slice
+// from the activations (`in`) in its prologue, exactly as quantize_rows does: per (token, group) the power of two
+// that puts the group's largest magnitude of x (x * norm weight with a norm) in [2^29, 2^30), four limbs of each
+// value; the RMSNorm factor of each token comes from the waves' partial sums of squares and scales the outputs.
+template <int BITS, int WG, int TT, int SM, typename ST, bool FUSE>
 __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(const uint8_t *__restrict__ codes, const ST *__restrict__ scales,
                                                       const int8_t *__restrict__ limbs,
                                                       const float *__restrict__ exps, const float *__restrict__ rsv,
-                                                      const int32_t *__restrict__ lsum, GemvOut out, int tokens,
-                                                      int rows, int cols, int tiles) {
+                                                      const int32_t *__restrict__ lsum, GemvIn in, GemvOut out,
+                                                      int tokens, int rows, int cols, int tiles) {
+    static_assert(!FUSE || (BITS == 8 && bres<SM>()), "fused limbs: int8 with B in registers");
     constexpr int CB = BITS == 8 ? 16 : 8;  // code bytes per lane per window
     constexpr int S = SM;
     constexpr int BRING = bring<TT, SM>();
@@ -82,11 +87,48 @@ __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(co
     const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int items = my_tiles * S;
     if (threadIdx.x < 4 * TT) best_s[threadIdx.x] = 0ull;  // read after the tiles' barriers
+    __shared__ float ssq_s[FUSE ? BW : 1][4 * TT];          // FUSE: the waves' partial sums of squares per token
+    __shared__ __align__(16) uint32_t tr_s[FUSE ? BW : 1][64][4];  // FUSE: a wave's limb transpose
 
     // the epilogue's token factors, loaded before the ring: a load issued after it would wait for all of it
     float rsl[TT];
 #pragma unroll
-    for (int pass = 0; pass < TT; ++pass) rsl[pass] = rsv[min(4 * pass + lane / 16, tokens - 1)];
+    for (int pass = 0; pass < TT; ++pass) rsl[pass] = FUSE ? 1.0f : rsv[min(4 * pass + lane / 16, tokens - 1)];
+
+    // FUSE: lane (q, t, L) (lane = 16 q + 4 t + L) loads values 16 q + 4 L .. + 3 of window w of token 4 j + t, for
+    // every window of the slice and token tile j; all loads unconditional (clamped) and issued before the ring
+    constexpr int FS = FUSE ? SM : 1, FT = FUSE ? TT : 1;
+    float fx[FS][FT][4], fw[FS][4];
+    if constexpr (FUSE) {
+        const bool bf = in.mode == IN_BF16, nrm = in.mode == IN_NORM;
+        const int ft = (lane & 15) >> 2, fl = lane & 3;
+#pragma unroll
+        for (int wl = 0; wl < SM; ++wl) {
+            const int col = 64 * min(wave * SM + wl, (cols >> 6) - 1) + 16 * q + 4 * fl;
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                const size_t at = (size_t)min(4 * j + ft, tokens - 1) * in.x_stride + col;
+                if (bf) {
+                    const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(in.x) + at);
+                    fx[wl][j][0] = __uint_as_float(u.x << 16);
+                    fx[wl][j][1] = __uint_as_float(u.x & 0xffff0000u);
+                    fx[wl][j][2] = __uint_as_float(u.y << 16);
+                    fx[wl][j][3] = __uint_as_float(u.y & 0xffff0000u);
+                } else {
+                    const float4 f = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(in.x) + at);
+                    fx[wl][j][0] = f.x;
+                    fx[wl][j][1] = f.y;
+                    fx[wl][j][2] = f.z;
+                    fx[wl][j][3] = f.w;
+                }
+            }
+            const float4 nw = *reinterpret_cast<const float4 *>(nrm ? in.norm + col : reinterpret_cast<const float *>(in.x) + col);
+            fw[wl][0] = nw.x;
+            fw[wl][1] = nw.y;
+            fw[wl][2] = nw.z;
+            fw[wl][3] = nw.w;
+        }
+    }
     // the limbs are in B-fragment order ([window][token tile][lane][16 bytes]); this lane's token in token tile j is
     // 4 j + c / 4, and a lane of a token past the batch reads the batch's last token (its sums are never written)
     const int ttiles = (tokens + 3) / 4;
@@ -108,7 +150,7 @@ __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(co
     // BRES: the wave's B fragments, window wl of the slice, token tile j; loaded before the ring, so the waits for
     // them come first in the counter and never drain it
     u32x4 bq[BRES ? S : 1][TT];
-    if constexpr (BRES) {
+    if constexpr (BRES && !FUSE) {
 #pragma unroll
         for (int wl = 0; wl < S; ++wl) {
             const int w = min(w0 + wl, windows - 1);
@@ -135,8 +177,10 @@ __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(co
                 rs_[slot / WG] = (floatx4){__uint_as_float(sv.x << 16), __uint_as_float(sv.x & 0xffff0000u),
                                            __uint_as_float(sv.y << 16), __uint_as_float(sv.y & 0xffff0000u)};
             }
+            if constexpr (!FUSE) {
 #pragma unroll
-            for (int j = 0; j < TT; ++j) re[slot / WG][j] = erow[j][w / WG];
+                for (int j = 0; j < TT; ++j) re[slot / WG][j] = erow[j][w / WG];
+            }
             if constexpr (BITS == 4) {
 #pragma unroll
                 for (int j = 0; j < TT; ++j) ro[slot / WG][j] = 8 * orow[j][(w / WG) * 4];
@@ -152,6 +196,69 @@ __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(co
     const int last = items > 0 ? items - 1 : 0;
 #pragma unroll
     for (int j = 0; j < BRING; ++j) load_item(min(j, last), j);
+
+    // FUSE: the slice's limbs (B fragments), group factors and the RMSNorm partial sums, while the ring is in flight
+    float egrp[FUSE ? SM / WG : 1][FT];
+    if constexpr (FUSE) {
+        const bool nrm = in.mode == IN_NORM;
+        const int ft = (lane & 15) >> 2, fl = lane & 3;
+        const int windows_ = cols >> 6;
+#pragma unroll
+        for (int j = 0; j < TT; ++j) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int gl = 0; gl < SM / WG; ++gl) {
+                float v[WG][4];
+                float mx = 0.0f;
+#pragma unroll
+                for (int ww = 0; ww < WG; ++ww) {
+                    const int wl = gl * WG + ww;
+                    const bool inrow = wave * SM + wl < windows_;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = inrow ? fx[wl][j][e] : 0.0f;
+                        ss += x * x;
+                        v[ww][e] = nrm ? x * fw[wl][e] : x;
+                        mx = fmaxf(mx, fabsf(v[ww][e]));
+                    }
+                }
+                // the group's largest magnitude: the 16 lanes of token t (L and q vary)
+                mx = fmaxf(mx, __shfl_xor(mx, 1));
+                mx = fmaxf(mx, __shfl_xor(mx, 2));
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                int sh = 0;
+                if (mx > 0.0f && mx < INFINITY) {
+                    int e;
+                    (void)frexpf(mx, &e);
+                    sh = 30 - e;
+                    sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+                }
+                const float up = ldexpf(1.0f, sh);
+                egrp[gl][j] = ldexpf(1.0f, -sh);
+#pragma unroll
+                for (int ww = 0; ww < WG; ++ww) {
+                    const int wl = gl * WG + ww;
+                    uint32_t wd[4];
+                    limbs4(__float2int_rn(v[ww][0] * up), __float2int_rn(v[ww][1] * up), __float2int_rn(v[ww][2] * up),
+                           __float2int_rn(v[ww][3] * up), wd);
+                    // quad transpose through LDS: lane L of the quad takes limb L of the quad's 16 values, in
+                    // column order (lane b + k holds values 4 k .. 4 k + 3)
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) tr_s[wave][(lane & ~3) + m][fl] = wd[m];
+                    __builtin_amdgcn_wave_barrier();
+                    bq[wl][j] = *reinterpret_cast<const u32x4 *>(&tr_s[wave][lane][0]);
+                    __builtin_amdgcn_wave_barrier();
+                }
+            }
+            // the wave's sum of squares of token 4 j + t: its 16 lanes
+            ss += __shfl_xor(ss, 1);
+            ss += __shfl_xor(ss, 2);
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if ((lane & 0x33) == 0) ssq_s[wave][4 * j + ft] = ss;
+        }
+    }
 
     floatx4 total[TT];
     int4v acc[TT];
@@ -201,7 +308,9 @@ __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(co
                 const floatx4 gsc = rs_[s / WG];
 #pragma unroll
                 for (int j = 0; j < TT; ++j) {
-                    const float gex = re[s / WG][j];
+                    float gex;
+                    if constexpr (FUSE) gex = egrp[s / WG][j];  // a round is the whole slice: s is the window in it
+                    else gex = re[s / WG][j];
                     if constexpr (BITS == 4) {
                         const int off = ro[s / WG][j];
                         acc[j] -= (int4v){off, off, off, off};
@@ -259,7 +368,17 @@ __global__ __launch_bounds__(64 * BW, batch_min_blocks<SM>()) void gemv_batch(co
         const int tn = p / (4 * TT * 8), tt = (p / 8) % (4 * TT), r = 2 * (p % 8);
         const int row = ((int)blockIdx.x + tn * (int)gridDim.x) * 16 + r;
         if (tt >= tokens) continue;
-        const float v0 = obuf[tn][tt][r], v1 = obuf[tn][tt][r + 1];
+        float v0 = obuf[tn][tt][r], v1 = obuf[tn][tt][r + 1];
+        if constexpr (FUSE) {
+            if (in.mode == IN_NORM) {
+                float ssum = 0.0f;
+#pragma unroll
+                for (int ww = 0; ww < BW; ++ww) ssum += ssq_s[ww][tt];
+                const float rs = 1.0f / sqrtf(ssum / (float)cols + in.eps);
+                v0 *= rs;
+                v1 *= rs;
+            }
+        }
         if (out.mode == OUT_SILU) {
             if (row < rows) reinterpret_cast<float *>(out.y)[(size_t)tt * out.y_stride + (row >> 1)] = silu_f(v0) * v1;
             continue;
@@ -306,54 +425,56 @@ bool gemv_batch_supported(const marin_quant_matrix *w, size_t tokens) {
 }
 
 template <int BITS, int WG, int TT, int SM, typename ST>
-static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
+static void launch_t(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     const int tiles = (int)(w->rows_padded / 16);
-    auto kern = gemv_batch<BITS, WG, TT, SM, ST>;
+    constexpr bool FUSE = BITS == 8 && bres<SM>();
+    const ActLimbs al = FUSE ? ActLimbs{nullptr, nullptr, nullptr, nullptr}
+                             : launch_quantize_act(g, in, tokens, w->cols, w->group, true);
+    auto kern = gemv_batch<BITS, WG, TT, SM, ST, FUSE>;
     int resident = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, 64 * BW, 0) != hipSuccess || resident < 1)
         resident = 1;
     const int blocks = std::max(std::min(tiles, std::min(resident, BATCH_BLOCKS_PER_CU) * std::max(g->cu_count, 1)),
                                 (tiles + OBUF_TILES - 1) / OBUF_TILES);
     kern<<<dim3((unsigned)blocks), dim3(64 * BW), 0, g->stream>>>(w->codes, (const ST *)w->scales, al.limbs, al.exps,
-                                                                   al.rs, al.lsum, out, (int)tokens, (int)w->rows,
+                                                                   al.rs, al.lsum, in, out, (int)tokens, (int)w->rows,
                                                                    (int)w->cols, tiles);
 }
 
 template <int BITS, int WG, int TT, typename ST>
-static void launch_sm(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
+static void launch_sm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     switch (batch_slice((int)(w->cols / 64))) {
-        case 4: launch_t<BITS, WG, TT, 4, ST>(g, w, al, out, tokens); break;
-        case 8: launch_t<BITS, WG, TT, 8, ST>(g, w, al, out, tokens); break;
-        case 12: launch_t<BITS, WG, TT, 12, ST>(g, w, al, out, tokens); break;
-        default: launch_t<BITS, WG, TT, 24, ST>(g, w, al, out, tokens); break;
+        case 4: launch_t<BITS, WG, TT, 4, ST>(g, w, in, out, tokens); break;
+        case 8: launch_t<BITS, WG, TT, 8, ST>(g, w, in, out, tokens); break;
+        case 12: launch_t<BITS, WG, TT, 12, ST>(g, w, in, out, tokens); break;
+        default: launch_t<BITS, WG, TT, 24, ST>(g, w, in, out, tokens); break;
     }
 }
 
 template <int BITS, typename ST>
-static void launch_bits(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out,
+static void launch_bits(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out,
                         size_t tokens) {
     const bool wg2 = w->group == 128;
     if (tokens <= 4) {
-        if (wg2) launch_sm<BITS, 2, 1, ST>(g, w, al, out, tokens);
-        else launch_sm<BITS, 1, 1, ST>(g, w, al, out, tokens);
+        if (wg2) launch_sm<BITS, 2, 1, ST>(g, w, in, out, tokens);
+        else launch_sm<BITS, 1, 1, ST>(g, w, in, out, tokens);
     } else {
-        if (wg2) launch_sm<BITS, 2, 2, ST>(g, w, al, out, tokens);
-        else launch_sm<BITS, 1, 2, ST>(g, w, al, out, tokens);
+        if (wg2) launch_sm<BITS, 2, 2, ST>(g, w, in, out, tokens);
+        else launch_sm<BITS, 1, 2, ST>(g, w, in, out, tokens);
     }
 }
 
 template <typename ST>
-static void launch_st(marin_gpu *g, const marin_quant_matrix *w, const ActLimbs &al, const GemvOut &out, size_t tokens) {
-    if (w->bits == 8) launch_bits<8, ST>(g, w, al, out, tokens);
-    else launch_bits<4, ST>(g, w, al, out, tokens);
+static void launch_st(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
+    if (w->bits == 8) launch_bits<8, ST>(g, w, in, out, tokens);
+    else launch_bits<4, ST>(g, w, in, out, tokens);
 }
 
 void launch_gemv_batch(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, const GemvOut &out, size_t tokens) {
     if (!gemv_batch_supported(w, tokens)) unsupported("batch product (2..8 tokens, int8 or int4, group 64 or 128)", 8, tokens);
     if (out.argmax && !out.argmax_each) unsupported("batch product greedy choice (one per token only)", 1, 0);
-    const ActLimbs al = launch_quantize_act(g, in, tokens, w->cols, w->group, true);
-    if (w->bf16_scales) launch_st<uint16_t>(g, w, al, out, tokens);
-    else launch_st<float>(g, w, al, out, tokens);
+    if (w->bf16_scales) launch_st<uint16_t>(g, w, in, out, tokens);
+    else launch_st<float>(g, w, in, out, tokens);
     const double act = in.mode == IN_BF16 ? 2.0 : 4.0, res = out.mode == OUT_BF16 ? 2.0 : 4.0;
     const double outs = out.mode == OUT_SILU ? (double)w->rows / 2 : (double)w->rows;
     const double bytes = (double)w->rows * w->row_bytes() + (double)w->rows * w->groups() * (w->bf16_scales ? 2 : 4) +
