@@ -471,6 +471,40 @@ def bench_paged(m, args) -> int:
     return 0
 
 
+SUB_MODES = [("linear", ["--linear"]), ("paged", ["--paged"]), ("moe", ["--moe"]), ("batch8", ["--batch", "8"]),
+             ("prefill", ["--prefill"])]
+
+
+def run_sub_benchmarks(args) -> dict:
+    """The other configurations, each in a child process of its own (before this process touches the GPU), so that
+    the default run's one JSON line carries them too: per mode its metric, value, unit, time per step and roofline."""
+    import subprocess
+    res = {}
+    for name, flags in SUB_MODES:
+        cmd = [sys.executable, "-u", os.path.abspath(__file__), *flags, "--no-cpu", "--seed", str(args.seed)]
+        print(f"[bench] sub-benchmark {name}: {' '.join(flags)}", file=sys.stderr, flush=True)
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        except subprocess.TimeoutExpired:
+            res[name] = {"error": "timed out"}
+            continue
+        lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+        if r.returncode != 0 or not lines:
+            res[name] = {"error": f"exit {r.returncode}", "stderr_tail": r.stderr[-400:]}
+            continue
+        d = json.loads(lines[-1])
+        keep = {k: d[k] for k in ("metric", "value", "unit", "ms_per_step", "dtype", "roofline", "config") if k in d}
+        if name == "moe":
+            keep["batches"] = {b: {k: v[k] for k in ("us_per_layer", "GBps", "attention_us_per_layer", "layer_us")}
+                               for b, v in d["batches"].items()}
+        if name == "linear":
+            keep["cases"] = [{k: c[k] for k in ("bits", "K", "N", "M", "us", "GBps")} for c in d["cases"]]
+        if name == "prefill":
+            keep["cases"] = d["cases"]
+        res[name] = keep
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -504,6 +538,8 @@ def main() -> int:
     ap.add_argument("--counters", action="store_true",
                     help="for rocprofv3 --pmc runs: set the mode's inputs up, then launch its measured work once, "
                          "eagerly, between two copy-probe markers, and exit (no timing, no JSON result line)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="the default run without the other configurations' sub-benchmarks")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's kernels one by one instead of replaying a HIP graph (for tracers)")
     args = ap.parse_args()
@@ -513,6 +549,11 @@ def main() -> int:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the one-GPU throughput is the reported value", file=sys.stderr)
         return 2
+
+    headline = not (args.moe or args.linear or args.paged or args.prefill or args.batch > 1 or args.probe_copy)
+    subs = None
+    if headline and not (args.headline_only or args.counters or args.no_graph or args.no_timing):
+        subs = run_sub_benchmarks(args)
 
     import marin_amd as m
     from marin_amd.qwen3 import SHAPES, Qwen3, weight_bytes
@@ -642,6 +683,8 @@ def main() -> int:
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(shape, args.prompt, args.kv == "f16")
+    if subs is not None:
+        line["configs"] = subs
     print(json.dumps(line), flush=True)
     return 0
 
