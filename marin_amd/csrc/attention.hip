@@ -1221,6 +1221,7 @@ static void launch_split_f(marin_gpu *g, const AttentionArgs &a, dim3 grid, int 
 }
 
 constexpr int DEC_BLOCKS_PER_CU = 1;  // one-token attention workgroups per compute unit the chunking aims at
+constexpr int DEC_ROUND_BLOCKS_PER_CU = 2;  // one-token attention workgroups resident per compute unit
 
 template <int F, int LPP, bool BF16IO, int R, bool FUSE, int U>
 static void launch_decode(marin_gpu *g, const AttentionArgs &a, dim3 grid, int chunk, int splits, float scale) {
@@ -1292,7 +1293,21 @@ static int decode_chunk(const AttentionArgs &a, int cu_count, int &splits) {
     const size_t per_unit = std::max<size_t>(1, (size_t)DEC_BLOCKS_PER_CU * std::max(cu_count, 1) / units);
     size_t chunk = (a.max_ctx + per_unit - 1) / per_unit;
     chunk = std::min<size_t>(std::max<size_t>(chunk, (size_t)step), (size_t)umax * step);
-    const size_t n = (a.max_ctx + chunk - 1) / chunk;
+    size_t n = (a.max_ctx + chunk - 1) / chunk;
+    // More workgroups than compute units (large batches, long contexts): they run in rounds of about
+    // DEC_ROUND_BLOCKS_PER_CU per unit, so the chunks are shortened until the workgroups fill whole rounds (17
+    // chunks per unit on 64 units would leave a third round almost empty; 24 shorter ones fill it).
+    const size_t cu = (size_t)std::max(cu_count, 1);
+    if (n * units > cu) {
+        const size_t cap = (size_t)DEC_ROUND_BLOCKS_PER_CU * cu;
+        const size_t rounds = (n * units + cap - 1) / cap;
+        const size_t want = std::min<size_t>(rounds * cap / units, (size_t)DEC_MAX_SPLITS);
+        if (want > n) {
+            chunk = (a.max_ctx + want - 1) / want;
+            chunk = std::max<size_t>((chunk + step - 1) / step * step, (size_t)step);
+            n = (a.max_ctx + chunk - 1) / chunk;
+        }
+    }
     if (n > (size_t)DEC_MAX_SPLITS) return 0;
     splits = (int)std::max<size_t>(n, 1);
     return (int)chunk;
