@@ -185,3 +185,25 @@ def test_decode_shapes_bf16_layout_within_the_north_star_tolerance(gpu, k, n, m_
     assert rel <= 1e-2, rel
     # bf16 output rounding bounds the error per element as well
     assert np.all(np.abs(got - exp) <= np.abs(exp) * 2 ** -7 + 1e-3 * np.abs(exp).max())
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (12288, 4096), (2048, 1000), (4096, 6144)])
+@pytest.mark.parametrize("tokens", [32, 100, 512])
+def test_prompt_products_with_bf16_scales_are_float32_grade(gpu, k, n, tokens):
+    """The prompt GEMM (32+ tokens: 22-bit activations in three limbs, workgroups of 128 or 256 rows, partial token
+    blocks) with bf16 weight scales and f32 activations: within 1e-6 of the largest output of the f64 product over the
+    same bf16-rounded scales, the bound of the reference's integer path (cuda/tests/quant.rs:76-118)."""
+    print(f"case k={k} n={n} tokens={tokens}", flush=True)
+    codes, scales = config1_matrix(k, n, 8)
+    sbf = o.f32_to_bf16_rne(scales)
+    s32 = o.bf16_to_f32(sbf)
+    x = values_fast(tokens * k, 41)
+    w = gpu.upload_quantized(n, k, 8, 128, codes, sbf, bf16_scales=True)
+    out = gpu.zeros(tokens * n)
+    gpu.matmul_quant(w, gpu.upload(x), tokens, out)
+    got = gpu.download(out).astype(np.float64).reshape(tokens, n)
+    c = codes.reshape(n, k).view(np.int8).astype(np.float64)
+    deq = (c.reshape(n, k // 128, 128) * s32.reshape(n, k // 128)[:, :, None]).reshape(n, k)
+    exp = x.astype(np.float64).reshape(tokens, k) @ deq.T
+    worst = np.abs(got - exp).max()
+    assert worst <= 1e-6 * np.abs(exp).max(), (worst, np.abs(exp).max())
