@@ -731,11 +731,9 @@ static void launch_prompt_wm(marin_gpu *g, const marin_quant_matrix *w, const in
     const int token_blocks = (int)((tokens + GP_TOK - 1) / GP_TOK);
     const unsigned grid = (unsigned)((row_blocks + 7) / 8 * 8 * token_blocks);
     const size_t lds = (size_t)S::STAGES * S::STAGE_BYTES;
-    static bool attr = false;  // dynamic LDS above 64 KiB must be allowed once per kernel
-    if (!attr) {
-        HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST, WM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
+    // dynamic LDS above 64 KiB must be allowed for the kernel (a host-side attribute, set on every launch so no
+    // process-wide state is kept; a prompt product takes tens of microseconds at least)
+    HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST, WM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     gemm_prompt<WG, ST, WM><<<grid, S::THREADS, lds, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
                                                                    (int)tokens, (int)w->rows, (int)w->cols, tiles,
                                                                    row_blocks, token_blocks);
