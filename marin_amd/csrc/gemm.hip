@@ -159,10 +159,12 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols,
     const int t = blockIdx.x;
     const int groups = cols / GCOLS;
     const bool norm = in.mode == IN_NORM;
+    // without a norm the columns may be split over gridDim.y workgroups of 4 QR_THREADS IT columns each
+    const int col0 = (int)blockIdx.y * 4 * QR_THREADS * IT;
     float v[IT][4], w[IT][4];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-        const int k = min(4 * ((int)threadIdx.x + QR_THREADS * it), cols - 4);  // clamped: loads stay unconditional
+        const int k = min(col0 + 4 * ((int)threadIdx.x + QR_THREADS * it), cols - 4);  // clamped: loads stay unconditional
         if (in.mode == IN_BF16) {
             const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(in.x) + (size_t)t * in.x_stride + k);
             v[it][0] = __uint_as_float(u.x << 16);
@@ -198,10 +200,10 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows(GemvIn in, int cols,
         for (int i = 0; i < QR_THREADS / 64; ++i) total += red[i];
         rs = 1.0f / sqrtf(total / (float)cols + in.eps);
     }
-    if (threadIdx.x == 0) rs_out[t] = rs;
+    if (threadIdx.x == 0 && blockIdx.y == 0) rs_out[t] = rs;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-        const int k = 4 * ((int)threadIdx.x + QR_THREADS * it);
+        const int k = col0 + 4 * ((int)threadIdx.x + QR_THREADS * it);
         const bool on = k < cols;
         float x[4];
 #pragma unroll
@@ -840,6 +842,14 @@ ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size
     int32_t *lsum = (int32_t *)(ws + limb_bytes + exp_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes + align16(tokens * (cols / group) * 16));
     const unsigned tt = (unsigned)ttiles;
+    if (frag && in.mode != IN_NORM) {
+        // no norm statistic: one workgroup per (token, 4096 columns)
+        const dim3 grid((unsigned)tokens, (unsigned)((cols + 4095) / 4096));
+        if (group == 128) quantize_rows<128, 1><<<grid, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt);
+        else quantize_rows<64, 1><<<grid, QR_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, lsum, tt);
+        g->launched();
+        return ActLimbs{limbs, exps, rs, lsum};
+    }
     if (frag && cols <= 4 * 4096) {
         const unsigned nt = (unsigned)tokens;
         const int it = (int)((cols + 4095) / 4096);
