@@ -30,6 +30,25 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int FA_ROWS = 16;  // query tokens per workgroup (one MFMA's rows)
+
+// Reductions over a row of 16 lanes with DPP (quad swaps, then the half-row and row mirrors): every step pairs lanes
+// symmetrically, so all 16 lanes end with the same value (a + b and b + a round alike).
+template <int CTRL>
+__device__ __forceinline__ float fa_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, fa_dpp<0xB1>(v));   // lanes xor 1
+    v = fmaxf(v, fa_dpp<0x4E>(v));   // lanes xor 2
+    v = fmaxf(v, fa_dpp<0x141>(v));  // half-row mirror (the other quad of 8 lanes)
+    return fmaxf(v, fa_dpp<0x140>(v));  // row mirror (the other 8 lanes)
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += fa_dpp<0xB1>(v);
+    v += fa_dpp<0x4E>(v);
+    v += fa_dpp<0x141>(v);
+    return v + fa_dpp<0x140>(v);
+}
 constexpr int FA_TILE = 32;  // positions per tile (one MFMA's k for P V)
 
 // RMSNorm(weight) + RoPE of one head by one wave, as in the decode kernels: lane i holds the pairs (i, i + hd/2).
@@ -274,8 +293,7 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
                 s[j][i] = v;
                 mx = fmaxf(mx, v);
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            mx = row16_max(mx);
             const float mn = fmaxf(m[i], mx);
             alpha[i] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
             float sum = 0.0f;
@@ -285,8 +303,7 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
                 s[j][i] = p;
                 sum += p;
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off);
+            sum = row16_sum(sum);
             l[i] = l[i] * alpha[i] + sum;
             m[i] = mn;
         }
