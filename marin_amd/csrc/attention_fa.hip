@@ -167,11 +167,12 @@ __global__ __launch_bounds__(576) void fa_prep(const void *__restrict__ qv, Attn
     }
 }
 
-// HD: head size (64 or 128); G: waves = q heads per kv head (1, 2, 4 or 8).
+// HD: head size (64 or 128); G: waves = q heads per kv head (1, 2, 4 or 8); RQ: 16-token row tiles per wave (every
+// key and value fragment read from LDS feeds RQ MFMAs, and a tile staged once serves 16 RQ tokens).
 // span 0: the workgroup walks every visible position and writes the output. span > 0 (a multiple of FA_TILE): split
 // blockIdx.z takes positions [z span, (z + 1) span) and leaves its rows' running maximum, sum and weighted values in
 // `part` ([splits][tokens][heads][HD] values, then [splits][tokens][heads] (max, sum)); fa_merge combines them.
-template <int HD, int G, bool BF16IO>
+template <int HD, int G, bool BF16IO, int RQ>
 __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict__ qh, const _Float16 *__restrict__ ql,
                                                   const float *__restrict__ qe, const uint64_t *__restrict__ table,
                                                   const uint32_t *__restrict__ ctx_lens, KvGeom geom, int tokens,
@@ -182,41 +183,46 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
     constexpr int CH = HD / 8;        // 16-byte chunks per row
     constexpr int KK = HD / 32;       // MFMAs along the head for one score block
     constexpr int DT = HD / 16;       // output tiles of 16 head values
+    constexpr int ROWS = FA_ROWS * RQ;
     __shared__ __align__(16) _Float16 kt[FA_TILE][KP];
     __shared__ __align__(16) _Float16 vt[HD][VP];
-    __shared__ __align__(16) float pl[G][FA_ROWS][FA_TILE + 4];
+    __shared__ __align__(16) float pl[G][ROWS][FA_TILE + 4];
     constexpr int NT = 64 * G;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, q = lane >> 4;
     const int kvh = blockIdx.y, h = kvh * G + wave;
-    const int t0 = blockIdx.x * FA_ROWS;
+    const int t0 = blockIdx.x * ROWS;
     const int ctx = (int)ctx_lens[0];
     const int base_pos = ctx - tokens;  // position of token 0
-    const int last_row = min(t0 + FA_ROWS - 1, tokens - 1);
+    const int last_row = min(t0 + ROWS - 1, tokens - 1);
     const int max_pos = base_pos + last_row;  // the workgroup's last visible position
     const uint64_t head_off = geom.layer_offset + (uint64_t)kvh * geom.head_bytes;
     const uint32_t pmask = (1u << geom.page_shift) - 1u;
 
-    // A operands of Q (rows = 16 tokens, this wave's head): lane row c, head values 32 kk + 8 q .. + 8
-    halfx8 aq_h[KK], aq_l[KK];
-    {
-        const int t = min(t0 + c, tokens - 1);
+    // A operands of Q (rows = 16 tokens of row tile r, this wave's head): lane row c, head values 32 kk + 8 q .. + 8
+    halfx8 aq_h[RQ][KK], aq_l[RQ][KK];
+#pragma unroll
+    for (int r = 0; r < RQ; ++r) {
+        const int t = min(t0 + 16 * r + c, tokens - 1);
         const size_t row = ((size_t)t * heads + h) * HD;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            aq_h[kk] = *reinterpret_cast<const halfx8 *>(qh + row + 32 * kk + 8 * q);
-            aq_l[kk] = *reinterpret_cast<const halfx8 *>(ql + row + 32 * kk + 8 * q);
+            aq_h[r][kk] = *reinterpret_cast<const halfx8 *>(qh + row + 32 * kk + 8 * q);
+            aq_l[r][kk] = *reinterpret_cast<const halfx8 *>(ql + row + 32 * kk + 8 * q);
         }
     }
-    // the C layout's rows 4 q + i: their tokens' positions and scale factors (scale x 2^-s, log2 domain)
-    int rpos[4];
-    float rsc[4];
+    // the C layout's rows 4 q + i of each row tile: their tokens' positions and scale factors (scale x 2^-s, log2
+    // domain)
+    int rpos[RQ][4];
+    float rsc[RQ][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = t0 + 4 * q + i;
-        rpos[i] = t < tokens ? base_pos + t : -1;  // rows past the prompt see nothing
-        rsc[i] = scale * qe[(size_t)min(t, tokens - 1) * heads + h];
-    }
+    for (int r = 0; r < RQ; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = t0 + 16 * r + 4 * q + i;
+            rpos[r][i] = t < tokens ? base_pos + t : -1;  // rows past the prompt see nothing
+            rsc[r][i] = scale * qe[(size_t)min(t, tokens - 1) * heads + h];
+        }
 
     // staging of one tile: chunk j of the tile (key or value row chunk), positions clamped to the visible ones
     constexpr int CHUNKS = 2 * FA_TILE * CH;
@@ -249,14 +255,17 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         }
     };
 
-    floatx4 o[DT];
+    floatx4 o[RQ][DT];
+    float m[RQ][4], l[RQ][4];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) o[d] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    float m[4], l[4];
+    for (int r = 0; r < RQ; ++r) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m[i] = -INFINITY;
-        l[i] = 0.0f;
+        for (int d = 0; d < DT; ++d) o[r][d] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            m[r][i] = -INFINITY;
+            l[r][i] = 0.0f;
+        }
     }
 
     const int p_begin = span ? (int)blockIdx.z * span : 0;
@@ -268,70 +277,81 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         __syncthreads();
         load_tile(min(p0 + FA_TILE, max_pos));  // past the last tile: a harmless reload of the last positions
 
-        // ---- scores: two 16-position blocks, hi and lo parts of q
-        floatx4 s[2];
+        // ---- scores: two 16-position blocks per row tile, hi and lo parts of q; each key fragment feeds RQ tiles
+        floatx4 s[RQ][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            floatx4 acc = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < RQ; ++r) s[r][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
                 const halfx8 bk = *reinterpret_cast<const halfx8 *>(&kt[16 * j + c][32 * kk + 8 * q]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_h[kk], bk, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_l[kk], bk, acc, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < RQ; ++r) {
+                    s[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_h[r][kk], bk, s[r][j], 0, 0, 0);
+                    s[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_l[r][kk], bk, s[r][j], 0, 0, 0);
+                }
             }
-            s[j] = acc;
         }
         // ---- online softmax of rows 4 q + i over this tile's positions (column c of block j: position p0 + 16 j + c)
-        float alpha[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float mx = -INFINITY;
+        for (int r = 0; r < RQ; ++r) {
+            float alpha[4];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int pos = p0 + 16 * j + c;
-                const float v = pos <= rpos[i] ? s[j][i] * rsc[i] : -INFINITY;
-                s[j][i] = v;
-                mx = fmaxf(mx, v);
+            for (int i = 0; i < 4; ++i) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int pos = p0 + 16 * j + c;
+                    const float v = pos <= rpos[r][i] ? s[r][j][i] * rsc[r][i] : -INFINITY;
+                    s[r][j][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+                mx = row16_max(mx);
+                const float mn = fmaxf(m[r][i], mx);
+                alpha[i] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[r][i] - mn);
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float p = s[r][j][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r][j][i] - mn);
+                    s[r][j][i] = p;
+                    sum += p;
+                }
+                sum = row16_sum(sum);
+                l[r][i] = l[r][i] * alpha[i] + sum;
+                m[r][i] = mn;
             }
-            mx = row16_max(mx);
-            const float mn = fmaxf(m[i], mx);
-            alpha[i] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
-            float sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float p = s[j][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[j][i] - mn);
-                s[j][i] = p;
-                sum += p;
-            }
-            sum = row16_sum(sum);
-            l[i] = l[i] * alpha[i] + sum;
-            m[i] = mn;
+            for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[r][d][i] *= alpha[i];
+            // P into the A layout (lane row c, positions 8 q .. + 8) through this wave's LDS tile
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pl[wave][16 * r + 4 * q + i][16 * j + c] = s[r][j][i];
         }
-#pragma unroll
-        for (int d = 0; d < DT; ++d)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[d][i] *= alpha[i];
-        // ---- P into the A layout (lane row c, positions 8 q .. + 8) through this wave's LDS tile, split hi + lo
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pl[wave][4 * q + i][16 * j + c] = s[j][i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // the wave's own LDS stores complete (lgkmcnt 0) before they are read
         __builtin_amdgcn_wave_barrier();
-        halfx8 ph, plo;
+        halfx8 ph[RQ], plo[RQ];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float p = pl[wave][c][8 * q + e];
-            const _Float16 hi = (_Float16)p;
-            ph[e] = hi;
-            plo[e] = (_Float16)(p - (float)hi);
-        }
+        for (int r = 0; r < RQ; ++r)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float p = pl[wave][16 * r + c][8 * q + e];
+                const _Float16 hi = (_Float16)p;
+                ph[r][e] = hi;
+                plo[r][e] = (_Float16)(p - (float)hi);
+            }
         // ---- O += P V: B operand lane column = head value 16 d + c, positions 8 q .. + 8 (transposed values)
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
             const halfx8 bv = *reinterpret_cast<const halfx8 *>(&vt[16 * d + c][8 * q]);
-            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bv, o[d], 0, 0, 0);
-            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, bv, o[d], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RQ; ++r) {
+                o[r][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[r], bv, o[r][d], 0, 0, 0);
+                o[r][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo[r], bv, o[r][d], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_wave_barrier();  // reads of pl done before the next tile overwrites it
     }
@@ -341,34 +361,38 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         const size_t plane = (size_t)tokens * heads;
         float *ml = part + (size_t)gridDim.z * plane * HD;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = t0 + 4 * q + i;
-            if (t >= tokens) continue;
-            const size_t unit = (size_t)blockIdx.z * plane + (size_t)t * heads + h;
+        for (int r = 0; r < RQ; ++r)
 #pragma unroll
-            for (int d = 0; d < DT; ++d) part[unit * HD + 16 * d + c] = o[d][i];
-            if (c == 0) *reinterpret_cast<float2 *>(ml + unit * 2) = make_float2(m[i], l[i]);
-        }
+            for (int i = 0; i < 4; ++i) {
+                const int t = t0 + 16 * r + 4 * q + i;
+                if (t >= tokens) continue;
+                const size_t unit = (size_t)blockIdx.z * plane + (size_t)t * heads + h;
+#pragma unroll
+                for (int d = 0; d < DT; ++d) part[unit * HD + 16 * d + c] = o[r][d][i];
+                if (c == 0) *reinterpret_cast<float2 *>(ml + unit * 2) = make_float2(m[r][i], l[r][i]);
+            }
         return;
     }
-    // ---- out: lane holds rows 4 q + i, head value 16 d + c
+    // ---- out: lane holds rows 4 q + i of each row tile, head value 16 d + c
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = t0 + 4 * q + i;
-        if (t >= tokens) continue;
-        const float inv = 1.0f / l[i];
-        const size_t row = ((size_t)t * heads + h) * HD;
+    for (int r = 0; r < RQ; ++r)
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            const float v = o[d][i] * inv;
-            if constexpr (BF16IO) {
-                const unsigned u = __float_as_uint(v);
-                reinterpret_cast<uint16_t *>(out)[row + 16 * d + c] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-            } else {
-                reinterpret_cast<float *>(out)[row + 16 * d + c] = v;
+        for (int i = 0; i < 4; ++i) {
+            const int t = t0 + 16 * r + 4 * q + i;
+            if (t >= tokens) continue;
+            const float inv = 1.0f / l[r][i];
+            const size_t row = ((size_t)t * heads + h) * HD;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const float v = o[r][d][i] * inv;
+                if constexpr (BF16IO) {
+                    const unsigned u = __float_as_uint(v);
+                    reinterpret_cast<uint16_t *>(out)[row + 16 * d + c] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+                } else {
+                    reinterpret_cast<float *>(out)[row + 16 * d + c] = v;
+                }
             }
         }
-    }
 }
 
 // The splits of every (token, head) row combined in split order: weights 2^(m_s - M) of the rows' maxima (log2
@@ -418,17 +442,19 @@ bool prefill_fa_fits(const AttentionArgs &a) {
            a.partial_floats * 4 >= prefill_fa_scratch(a.tokens, a.heads, hd);
 }
 
+constexpr int FA_RQ = 1;  // 16-token row tiles per wave (2 measured slower: one wave per SIMD from its registers)
+
 template <int HD, int G>
 static void launch_fa_t(marin_gpu *g, const AttentionArgs &a, const _Float16 *qh, const _Float16 *ql, const float *qe,
                         float scale, int splits, float *part) {
-    dim3 grid((unsigned)((a.tokens + FA_ROWS - 1) / FA_ROWS), (unsigned)a.kv_heads, (unsigned)splits);
+    dim3 grid((unsigned)((a.tokens + FA_ROWS * FA_RQ - 1) / (FA_ROWS * FA_RQ)), (unsigned)a.kv_heads, (unsigned)splits);
     const int span = splits > 1 ? FA_SPAN : 0;
     if (a.bf16_io)
-        fa_prefill<HD, G, true><<<grid, 64 * G, 0, g->stream>>>(qh, ql, qe, a.tables, a.ctx, a.geom, (int)a.tokens,
-                                                                (int)a.heads, (int)a.kv_heads, scale, span, part, a.out);
+        fa_prefill<HD, G, true, FA_RQ><<<grid, 64 * G, 0, g->stream>>>(qh, ql, qe, a.tables, a.ctx, a.geom, (int)a.tokens,
+                                                                       (int)a.heads, (int)a.kv_heads, scale, span, part, a.out);
     else
-        fa_prefill<HD, G, false><<<grid, 64 * G, 0, g->stream>>>(qh, ql, qe, a.tables, a.ctx, a.geom, (int)a.tokens,
-                                                                 (int)a.heads, (int)a.kv_heads, scale, span, part, a.out);
+        fa_prefill<HD, G, false, FA_RQ><<<grid, 64 * G, 0, g->stream>>>(qh, ql, qe, a.tables, a.ctx, a.geom, (int)a.tokens,
+                                                                        (int)a.heads, (int)a.kv_heads, scale, span, part, a.out);
     if (splits > 1) {
         g->launched(marin_gpu::ATTENTION, a.bytes_hint, "fa_prefill");
         const unsigned rows = (unsigned)(a.tokens * a.heads);
