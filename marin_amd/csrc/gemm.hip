@@ -506,16 +506,21 @@ static_assert(GP_TOK <= 64, "one token factor per lane");
 // The workgroup's shape for GP_WM row waves (4: 256 rows; 2: 128 rows, for matrices whose 256-row blocks would leave
 // compute units idle) and its stage layout: A [tile][64 lanes][16 B] | B [token tile][limb][64 lanes][16 B] |
 // scales [rows] f32 (bf16: the first half) | token factors [tokens] f32 | pad (the spare loads' target)
-template <int WM>
+template <int WM, int GS>
 struct GpShape {
     static constexpr int ROWS = WM * GP_RT * 16, TILES = ROWS / 16;
     static constexpr int WAVES = WM * GP_WN, THREADS = 64 * WAVES;
-    static constexpr int STAGES = WM == 4 ? 4 : 3;  // 128-row workgroups: 3 stages, so two fit a compute unit
+    // stages of GS windows: one-window stages 4 deep (3 for 128-row workgroups, so two fit a compute unit),
+    // group stages 2 deep
+    static constexpr int STAGES = GS > 1 ? 2 : (WM == 4 ? 4 : 3);
     static constexpr int A_BYTES = TILES * 1024, B_BYTES = GP_WN * GP_TN * GP_L * 1024;
-    static constexpr int SC_OFF = A_BYTES + B_BYTES, EX_OFF = SC_OFF + 1024, PAD_OFF = EX_OFF + GP_TOK * 4;
+    static constexpr int WIN_BYTES = A_BYTES + B_BYTES;  // one window's operands inside a stage
+    static constexpr int SC_OFF = GS * WIN_BYTES, EX_OFF = SC_OFF + 1024, PAD_OFF = EX_OFF + GP_TOK * 4;
     static constexpr int STAGE_BYTES = (PAD_OFF + 1024 + 255) / 256 * 256;
-    // loads per window: A tiles, B fragments, scales, token factors; padded to a whole number per wave
-    static constexpr int LOADS = TILES + GP_WN * GP_TN * GP_L + 2;
+    // loads per stage: A tiles and B fragments of each window, scales, token factors; padded to a whole number per
+    // wave
+    static constexpr int PER_WIN = TILES + GP_WN * GP_TN * GP_L;
+    static constexpr int LOADS = GS * PER_WIN + 2;
     static constexpr int LPW = (LOADS + WAVES - 1) / WAVES;
     static_assert(ROWS * 4 <= 1024, "scales of one stage");
 };
@@ -523,8 +528,8 @@ struct GpShape {
 typedef __attribute__((address_space(3))) void gp_lds_t;
 typedef __attribute__((address_space(1))) const void gp_glb_t;
 
-template <int WG, typename ST, int WM>
-__global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_prompt(const uint8_t *__restrict__ codes,
+template <int WG, typename ST, int WM, int GS>
+__global__ __launch_bounds__((GpShape<WM, GS>::THREADS), WM == 4 ? 1 : 2) void gemm_prompt(const uint8_t *__restrict__ codes,
                                                               const ST *__restrict__ scales,
                                                               const int8_t *__restrict__ limbs,
                                                               const float *__restrict__ exps,
@@ -532,7 +537,8 @@ __global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_pr
                                                               int rows, int cols, int tiles, int row_blocks,
                                                               int token_blocks) {
     extern __shared__ __align__(256) unsigned char gp_lds[];
-    using S = GpShape<WM>;
+    using S = GpShape<WM, GS>;
+    static_assert(GS == 1 || GS == WG, "stages of one window or of one group");
     constexpr int GP_WM = WM, GP_TILES = S::TILES, GP_WAVES = S::WAVES, GP_LPW = S::LPW;
     constexpr int GP_A_BYTES = S::A_BYTES, GP_SC_OFF = S::SC_OFF, GP_EX_OFF = S::EX_OFF, GP_PAD_OFF = S::PAD_OFF;
     constexpr int GP_STAGE_BYTES = S::STAGE_BYTES, GP_STAGES = S::STAGES;
@@ -555,20 +561,24 @@ __global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_pr
     // out once (the loop adds a wave-uniform offset), its kind and its LDS offset inside a stage.
     const unsigned char *src[GP_LPW];
     int kind[GP_LPW], dst[GP_LPW];
+    int sub_w[GP_LPW];  // the slot's window inside the stage
 #pragma unroll
     for (int i = 0; i < GP_LPW; ++i) {
-        const int k = wave * GP_LPW + i;  // wave-uniform
+        const int k0 = wave * GP_LPW + i;  // wave-uniform
+        const int u = k0 < GS * S::PER_WIN ? k0 / S::PER_WIN : 0;
+        const int k = k0 < GS * S::PER_WIN ? k0 % S::PER_WIN : k0 - GS * S::PER_WIN + S::PER_WIN;
+        sub_w[i] = u;
         if (k < GP_TILES) {
             const int tl = min(tbase + k, tiles - 1);
             src[i] = codes + (size_t)tl * tile_bytes + 16 * lane;
             kind[i] = 0;
-            dst[i] = k * 1024;
+            dst[i] = u * S::WIN_BYTES + k * 1024;
         } else if (k < GP_TILES + GP_WN * GP_TN * GP_L) {
             const int f = k - GP_TILES, j = f / GP_L, l = f % GP_L;
             const int tok = min(t0 + 16 * j + c, tokens - 1);
             src[i] = reinterpret_cast<const unsigned char *>(limbs + ((size_t)tok * GP_L + l) * cols + 16 * q);
             kind[i] = 1;
-            dst[i] = GP_A_BYTES + f * 1024;
+            dst[i] = u * S::WIN_BYTES + GP_A_BYTES + f * 1024;
         } else if (k == GP_TILES + GP_WN * GP_TN * GP_L) {
             // 16 bytes a lane: f32 scales of 4 rows (lane l: tile l / 4), bf16 of 8 rows (lanes 32+ repeat)
             const int r0 = sizeof(ST) == 4 ? 4 * lane : 8 * (lane & 31);
@@ -584,12 +594,13 @@ __global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_pr
         }
     }
     // the wave's loads of window `win` into stage `st` (a window past the last loads the last one again)
-    auto issue = [&](int win, int st) {
-        win = min(win, windows - 1);
-        const int g = win / WG;
+    auto issue = [&](int unit, int st) {  // stage unit `unit`: windows unit GS .. + GS - 1
+        const int w0 = min(unit * GS, windows - GS);
+        const int g = w0 / WG;
         unsigned char *base = gp_lds + st * GP_STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < GP_LPW; ++i) {
+            const int win = w0 + sub_w[i];
             if (kind[i] == 0)
                 __builtin_amdgcn_global_load_lds((gp_glb_t *)(src[i] + (size_t)win * 1024), (gp_lds_t *)(base + dst[i]), 16, 0, 0);
             else if (kind[i] == 1)
@@ -611,8 +622,8 @@ __global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_pr
     // magnitude), then the limbs recombined once: l0 + 256 l1 in an integer (below 2^30), + 65536 l2 in f32, scaled
     // by weight scale x the token's 2^-s.
     int4v acc[GP_RT][GP_TN][GP_L];
-    auto mfmas = [&](int st) {
-        const unsigned char *base = gp_lds + st * GP_STAGE_BYTES;
+    auto mfmas = [&](int st, int u) {
+        const unsigned char *base = gp_lds + st * GP_STAGE_BYTES + u * S::WIN_BYTES;
         int4v af[GP_RT];
 #pragma unroll
         for (int rt = 0; rt < GP_RT; ++rt)
@@ -673,12 +684,15 @@ __global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_pr
 #pragma unroll
         for (int w = 0; w < WG; ++w) {
             const int i = g * WG + w;
-            // at most the loads of windows i + 1 .. i + GP_STAGES - 2 outstanding
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((GP_STAGES - 2) * GP_LPW) : "memory");
-            __builtin_amdgcn_s_barrier();
-            issue(i + GP_STAGES - 1, (i + GP_STAGES - 1) % GP_STAGES);
-            mfmas(i % GP_STAGES);
-            if (w == WG - 1) finish(i % GP_STAGES);
+            if (GS == 1 || w == 0) {
+                const int unit = i / GS;
+                // at most the loads of units unit + 1 .. unit + GP_STAGES - 2 outstanding
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"((GP_STAGES - 2) * GP_LPW) : "memory");
+                __builtin_amdgcn_s_barrier();
+                issue(unit + GP_STAGES - 1, (unit + GP_STAGES - 1) % GP_STAGES);
+            }
+            mfmas((i / GS) % GP_STAGES, i % GS);
+            if (w == WG - 1) finish((i / GS) % GP_STAGES);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the spare loads past the last window land before exit
@@ -724,10 +738,10 @@ __global__ __launch_bounds__(GpShape<WM>::THREADS, WM == 4 ? 1 : 2) void gemm_pr
     }
 }
 
-template <int WG, typename ST, int WM>
+template <int WG, typename ST, int WM, int GS>
 static void launch_prompt_wm(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
                              const float *rs, const GemvOut &out, size_t tokens) {
-    using S = GpShape<WM>;
+    using S = GpShape<WM, GS>;
     const int tiles = (int)(w->rows_padded / 16);
     const int row_blocks = (int)((w->rows_padded + S::ROWS - 1) / S::ROWS);
     const int token_blocks = (int)((tokens + GP_TOK - 1) / GP_TOK);
@@ -735,8 +749,8 @@ static void launch_prompt_wm(marin_gpu *g, const marin_quant_matrix *w, const in
     const size_t lds = (size_t)S::STAGES * S::STAGE_BYTES;
     // dynamic LDS above 64 KiB must be allowed for the kernel (a host-side attribute, set on every launch so no
     // process-wide state is kept; a prompt product takes tens of microseconds at least)
-    HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST, WM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    gemm_prompt<WG, ST, WM><<<grid, S::THREADS, lds, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
+    HIP_CHECK(hipFuncSetAttribute((const void *)gemm_prompt<WG, ST, WM, GS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    gemm_prompt<WG, ST, WM, GS><<<grid, S::THREADS, lds, g->stream>>>(w->codes, (const ST *)w->scales, limbs, exps, rs, out,
                                                                    (int)tokens, (int)w->rows, (int)w->cols, tiles,
                                                                    row_blocks, token_blocks);
 }
@@ -746,9 +760,11 @@ template <int WG, typename ST>
 static void launch_prompt_t(marin_gpu *g, const marin_quant_matrix *w, const int8_t *limbs, const float *exps,
                             const float *rs, const GemvOut &out, size_t tokens) {
     const size_t token_blocks = (tokens + GP_TOK - 1) / GP_TOK;
-    const size_t big = (w->rows_padded + GpShape<4>::ROWS - 1) / GpShape<4>::ROWS * token_blocks;
-    if (2 * big > (size_t)std::max(g->cu_count, 1)) launch_prompt_wm<WG, ST, 4>(g, w, limbs, exps, rs, out, tokens);
-    else launch_prompt_wm<WG, ST, 2>(g, w, limbs, exps, rs, out, tokens);
+    const size_t big = (w->rows_padded + GpShape<4, 1>::ROWS - 1) / GpShape<4, 1>::ROWS * token_blocks;
+    // 128-row workgroups stage whole groups, two deep (measured faster there: o 74.5 -> 71.2 us, down 194 -> 183 us
+    // at 512 tokens); 256-row ones stage single windows, four deep (group stages were slower for them)
+    if (2 * big > (size_t)std::max(g->cu_count, 1)) launch_prompt_wm<WG, ST, 4, 1>(g, w, limbs, exps, rs, out, tokens);
+    else launch_prompt_wm<WG, ST, 2, WG>(g, w, limbs, exps, rs, out, tokens);
 }
 
 bool gemm_layout_ok(const marin_quant_matrix *w) {
