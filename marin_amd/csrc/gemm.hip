@@ -539,7 +539,7 @@ __global__ __launch_bounds__((GpShape<WM, GS>::THREADS), WM == 4 ? 1 : 2) void g
     extern __shared__ __align__(256) unsigned char gp_lds[];
     using S = GpShape<WM, GS>;
     static_assert(GS == 1 || GS == WG, "stages of one window or of one group");
-    constexpr int GP_WM = WM, GP_TILES = S::TILES, GP_WAVES = S::WAVES, GP_LPW = S::LPW;
+    constexpr int GP_WM = WM, GP_TILES = S::TILES, GP_LPW = S::LPW;
     constexpr int GP_A_BYTES = S::A_BYTES, GP_SC_OFF = S::SC_OFF, GP_EX_OFF = S::EX_OFF, GP_PAD_OFF = S::PAD_OFF;
     constexpr int GP_STAGE_BYTES = S::STAGE_BYTES, GP_STAGES = S::STAGES;
     // XCD-aware numbering: ids in runs of 8 x token_blocks; within a run, id % 8 picks the row block, id / 8 the
