@@ -26,6 +26,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int QA_THREADS = 256;
+// quantize_act's grid: a workgroup per (token, 1024 columns)
+inline dim3 qa_grid(size_t tokens, size_t cols) { return dim3((unsigned)tokens, (unsigned)((cols + 1023) / 1024)); }
 constexpr int GM_WAVES = 4;       // waves along the rows (128 rows per workgroup)
 constexpr int GM_ROW_TILES = 2;   // 16-row tiles per wave
 // Token halves of a workgroup: blocks of 64+ tokens take two sets of row waves, one per 32 tokens, so each code
@@ -44,7 +46,10 @@ __device__ __forceinline__ unsigned long long choice_key(float v, int row) {
 
 }  // namespace
 
-// One token row per workgroup. GCOLS = quantization group width (a multiple of 4, at most 4 * 64).
+// grid (tokens, column slices of 1024): workgroup (t, y) quantizes columns [1024 y, 1024 (y + 1)) of token row t
+// (GPI groups of GCOLS columns, GPI * GCOLS = 1024), one load per thread, so no workgroup walks a long row alone;
+// workgroup (t, 0) also computes the row's RMSNorm factor. GCOLS = quantization group width (a multiple of 4, at most
+// 4 * 64).
 // FRAG false: limbs [token][limb][column]. FRAG true (the batch product): the limbs already in B-operand order,
 // [window][token tile][64 lanes][16 bytes] with lane 16 q + 4 (token % 4) + limb holding columns 64 w + 16 q .. + 16,
 // so each B fragment is one contiguous KiB; `ttiles` = token tiles of 4.
@@ -77,8 +82,9 @@ __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, 
     };
     const bool norm = in.mode == IN_NORM;
     float rs = 1.0f;
-    if (norm) {
+    if (norm && blockIdx.y == 0) {
         float ss = 0.0f;
+#pragma unroll 4
         for (int k = threadIdx.x * 4; k < cols; k += QA_THREADS * 4) {
             float v[4];
             load4(k, v);
@@ -92,9 +98,10 @@ __global__ __launch_bounds__(QA_THREADS) void quantize_act(GemvIn in, int cols, 
         for (int w = 0; w < QA_THREADS / 64; ++w) total += red[w];
         rs = 1.0f / sqrtf(total / (float)cols + in.eps);
     }
-    if (threadIdx.x == 0) rs_out[t] = rs;
+    if (threadIdx.x == 0 && blockIdx.y == 0) rs_out[t] = rs;
     constexpr int GPI = QA_THREADS / TPG;  // groups per iteration
-    for (int g0 = 0; g0 < groups; g0 += GPI) {
+    static_assert(GPI * GCOLS == 1024, "column slices of 1024");
+    for (int g0 = (int)blockIdx.y * GPI; g0 < groups; g0 += GPI * (int)gridDim.y) {
         const int g = g0 + (int)threadIdx.x / TPG;
         const int k = g * GCOLS + ((int)threadIdx.x % TPG) * 4;
         const bool on = g < groups;
@@ -811,8 +818,8 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
     const bool wg2 = w->group == 128;
     if (prompt) {
-        if (wg2) quantize_act<128, false, GP_L><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
-        else quantize_act<64, false, GP_L><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+        if (wg2) quantize_act<128, false, GP_L><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+        else quantize_act<64, false, GP_L><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
         g->launched();
         if (w->bf16_scales) {
             if (wg2) launch_prompt_t<2, uint16_t>(g, w, limbs, exps, rs, out, tokens);
@@ -822,8 +829,8 @@ void launch_gemm(marin_gpu *g, const marin_quant_matrix *w, const GemvIn &in, co
             else launch_prompt_t<1, float>(g, w, limbs, exps, rs, out, tokens);
         }
     } else {
-    if (w->group == 128) quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
-    else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+    if (w->group == 128) quantize_act<128, false><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+    else quantize_act<64, false><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
     g->launched();
     if (w->bf16_scales) {
         if (wg2) launch_t<2, uint16_t>(g, w, limbs, exps, rs, out, tokens);
@@ -888,11 +895,11 @@ ActLimbs launch_quantize_act(marin_gpu *g, const GemvIn &in, size_t tokens, size
         return ActLimbs{limbs, exps, rs, lsum};
     }
     if (group == 128) {
-        if (frag) quantize_act<128, true><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
-        else quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+        if (frag) quantize_act<128, true><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+        else quantize_act<128, false><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
     } else {
-        if (frag) quantize_act<64, true><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
-        else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+        if (frag) quantize_act<64, true><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
+        else quantize_act<64, false><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, tt);
     }
     g->launched();
     return ActLimbs{limbs, exps, rs, nullptr};
@@ -923,8 +930,8 @@ void launch_moe_gate_up(marin_gpu *g, const marin_quant_matrix *w, const GemvIn 
     int8_t *limbs = (int8_t *)ws;
     float *exps = (float *)(ws + limb_bytes);
     float *rs = (float *)(ws + limb_bytes + exp_bytes);
-    if (w->group == 128) quantize_act<128, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
-    else quantize_act<64, false><<<(unsigned)tokens, QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+    if (w->group == 128) quantize_act<128, false><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
+    else quantize_act<64, false><<<qa_grid(tokens, cols), QA_THREADS, 0, g->stream>>>(in, (int)cols, limbs, exps, rs, 0);
     g->launched();
     MoePlanView pv;
     pv.plan = plan;
