@@ -7,7 +7,7 @@
 // value into the cache, rounded as every cache store.
 //
 // fa_prefill: a workgroup per (16 query tokens, kv head, span of 1024 positions when the context is longer), a wave
-// per q head of the group. Key and value tiles of 32
+// per q head of the group. Key and value tiles of 64
 // positions are staged in LDS once for the whole group (keys position-major, values transposed), the next tile's
 // loads in flight while the current one is used. Per tile and wave: S = Q K^T on v_mfma_f32_16x16x32_f16 (hi and lo
 // parts: keys are exact in f16, so the scores are f32-grade), causal mask, online softmax in the log2 domain with the
@@ -49,7 +49,8 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += fa_dpp<0x141>(v);
     return v + fa_dpp<0x140>(v);
 }
-constexpr int FA_TILE = 32;  // positions per tile (one MFMA's k for P V)
+constexpr int FA_TILE = 64;  // positions per tile: FA_TILE / 16 score blocks, FA_TILE / 32 MFMA k-steps of P V
+static_assert(FA_TILE % 32 == 0, "whole k-steps of P V");
 
 // RMSNorm(weight) + RoPE of one head by one wave, as in the decode kernels: lane i holds the pairs (i, i + hd/2).
 __device__ __forceinline__ void fa_norm_rope(const float *__restrict__ src, const float *__restrict__ w,
@@ -184,6 +185,8 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
     constexpr int KK = HD / 32;       // MFMAs along the head for one score block
     constexpr int DT = HD / 16;       // output tiles of 16 head values
     constexpr int ROWS = FA_ROWS * RQ;
+    constexpr int TB = FA_TILE / 16;  // 16-position score blocks per tile
+    constexpr int KS = FA_TILE / 32;  // k-steps of 32 positions for P V
     __shared__ __align__(16) _Float16 kt[FA_TILE][KP];
     __shared__ __align__(16) _Float16 vt[HD][VP];
     __shared__ __align__(16) float pl[G][ROWS][FA_TILE + 4];
@@ -278,9 +281,9 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         load_tile(min(p0 + FA_TILE, max_pos));  // past the last tile: a harmless reload of the last positions
 
         // ---- scores: two 16-position blocks per row tile, hi and lo parts of q; each key fragment feeds RQ tiles
-        floatx4 s[RQ][2];
+        floatx4 s[RQ][TB];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TB; ++j) {
 #pragma unroll
             for (int r = 0; r < RQ; ++r) s[r][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
             for (int i = 0; i < 4; ++i) {
                 float mx = -INFINITY;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < TB; ++j) {
                     const int pos = p0 + 16 * j + c;
                     const float v = pos <= rpos[r][i] ? s[r][j][i] * rsc[r][i] : -INFINITY;
                     s[r][j][i] = v;
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
                 alpha[i] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[r][i] - mn);
                 float sum = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < TB; ++j) {
                     const float p = s[r][j][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r][j][i] - mn);
                     s[r][j][i] = p;
                     sum += p;
@@ -327,30 +330,35 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
                 for (int i = 0; i < 4; ++i) o[r][d][i] *= alpha[i];
             // P into the A layout (lane row c, positions 8 q .. + 8) through this wave's LDS tile
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TB; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) pl[wave][16 * r + 4 * q + i][16 * j + c] = s[r][j][i];
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // the wave's own LDS stores complete (lgkmcnt 0) before they are read
         __builtin_amdgcn_wave_barrier();
-        halfx8 ph[RQ], plo[RQ];
+        halfx8 ph[RQ][KS], plo[RQ][KS];
 #pragma unroll
         for (int r = 0; r < RQ; ++r)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float p = pl[wave][16 * r + c][8 * q + e];
-                const _Float16 hi = (_Float16)p;
-                ph[r][e] = hi;
-                plo[r][e] = (_Float16)(p - (float)hi);
-            }
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float p = pl[wave][16 * r + c][32 * ks + 8 * q + e];
+                    const _Float16 hi = (_Float16)p;
+                    ph[r][ks][e] = hi;
+                    plo[r][ks][e] = (_Float16)(p - (float)hi);
+                }
         // ---- O += P V: B operand lane column = head value 16 d + c, positions 8 q .. + 8 (transposed values)
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
-            const halfx8 bv = *reinterpret_cast<const halfx8 *>(&vt[16 * d + c][8 * q]);
 #pragma unroll
-            for (int r = 0; r < RQ; ++r) {
-                o[r][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[r], bv, o[r][d], 0, 0, 0);
-                o[r][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo[r], bv, o[r][d], 0, 0, 0);
+            for (int ks = 0; ks < KS; ++ks) {
+                const halfx8 bv = *reinterpret_cast<const halfx8 *>(&vt[16 * d + c][32 * ks + 8 * q]);
+#pragma unroll
+                for (int r = 0; r < RQ; ++r) {
+                    o[r][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[r][ks], bv, o[r][d], 0, 0, 0);
+                    o[r][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo[r][ks], bv, o[r][d], 0, 0, 0);
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();  // reads of pl done before the next tile overwrites it
