@@ -227,33 +227,77 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
             rsc[r][i] = scale * qe[(size_t)min(t, tokens - 1) * heads + h];
         }
 
-    // staging of one tile: chunk j of the tile (key or value row chunk), positions clamped to the visible ones
+    // staging of one tile: chunk j of the tile (key or value row chunk), positions clamped to the visible ones.
+    // TRV (when the threads divide them evenly): the value chunks go in units of 4 consecutive positions x 8 head
+    // values per thread, transposed in registers and stored as 8 rows of 4 halves (8-byte stores) instead of 8
+    // single halves per chunk.
     constexpr int CHUNKS = 2 * FA_TILE * CH;
     constexpr int SLOTS = (CHUNKS + NT - 1) / NT;
+    constexpr int KCH = FA_TILE * CH, VU = KCH / 4;  // key chunks, value units
+    constexpr bool TRV = KCH % NT == 0 && VU % NT == 0;
+    constexpr int KPT = KCH / NT, VPT = VU / NT;  // (TRV) key chunks and value units per thread
     u32x4 stage[SLOTS];
+    auto load_chunk = [&](int which, int r, int ch, int p0) {
+        const uint32_t pos = (uint32_t)min(p0 + r, max_pos);
+        const uint64_t page = table[pos >> geom.page_shift] + head_off + (which ? geom.value_offset : 0) +
+                              (uint64_t)(pos & pmask) * HD * 2;
+        return *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint8_t *>(page) + 16 * ch);
+    };
     auto load_tile = [&](int p0) {
+        if constexpr (TRV) {
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-            const int j = min((int)threadIdx.x + s * NT, CHUNKS - 1);  // clamped: the loads stay unconditional
-            const int which = j / (FA_TILE * CH), r = (j / CH) % FA_TILE, ch = j % CH;
-            const uint32_t pos = (uint32_t)min(p0 + r, max_pos);
-            const uint64_t page = table[pos >> geom.page_shift] + head_off + (which ? geom.value_offset : 0) +
-                                  (uint64_t)(pos & pmask) * HD * 2;
-            stage[s] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint8_t *>(page) + 16 * ch);
+            for (int s = 0; s < KPT; ++s) {
+                const int j = (int)threadIdx.x + s * NT;
+                stage[s] = load_chunk(0, j / CH, j % CH, p0);
+            }
+#pragma unroll
+            for (int v = 0; v < VPT; ++v) {
+                const int u = (int)threadIdx.x + v * NT, ch = u / (FA_TILE / 4), pg = u % (FA_TILE / 4);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) stage[KPT + 4 * v + k] = load_chunk(1, 4 * pg + k, ch, p0);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) {
+                const int j = min((int)threadIdx.x + s * NT, CHUNKS - 1);  // clamped: the loads stay unconditional
+                stage[s] = load_chunk(j / (FA_TILE * CH), (j / CH) % FA_TILE, j % CH, p0);
+            }
         }
     };
     auto store_tile = [&]() {
+        if constexpr (TRV) {
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-            const int j = (int)threadIdx.x + s * NT;
-            if (j >= CHUNKS) continue;
-            const int which = j / (FA_TILE * CH), r = (j / CH) % FA_TILE, ch = j % CH;
-            if (which == 0) {
-                *reinterpret_cast<u32x4 *>(&kt[r][8 * ch]) = stage[s];
-            } else {
-                const halfx8 v = __builtin_bit_cast(halfx8, stage[s]);
+            for (int s = 0; s < KPT; ++s) {
+                const int j = (int)threadIdx.x + s * NT;
+                *reinterpret_cast<u32x4 *>(&kt[j / CH][8 * (j % CH)]) = stage[s];
+            }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vt[8 * ch + e][r] = v[e];
+            for (int v = 0; v < VPT; ++v) {
+                const int u = (int)threadIdx.x + v * NT, ch = u / (FA_TILE / 4), pg = u % (FA_TILE / 4);
+                const u32x4 *c4 = &stage[KPT + 4 * v];  // positions 4 pg .. + 3, head values 8 ch .. + 7
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int w = e / 2;
+                    auto pair = [&](const u32x4 &a, const u32x4 &b) {  // half e of a (low), of b (high)
+                        return (e & 1) ? (a[w] >> 16) | (b[w] & 0xffff0000u) : (a[w] & 0xffffu) | (b[w] << 16);
+                    };
+                    *reinterpret_cast<uint2 *>(&vt[8 * ch + e][4 * pg]) =
+                        make_uint2(pair(c4[0], c4[1]), pair(c4[2], c4[3]));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) {
+                const int j = (int)threadIdx.x + s * NT;
+                if (j >= CHUNKS) continue;
+                const int which = j / (FA_TILE * CH), r = (j / CH) % FA_TILE, ch = j % CH;
+                if (which == 0) {
+                    *reinterpret_cast<u32x4 *>(&kt[r][8 * ch]) = stage[s];
+                } else {
+                    const halfx8 v = __builtin_bit_cast(halfx8, stage[s]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) vt[8 * ch + e][r] = v[e];
+                }
             }
         }
     };
