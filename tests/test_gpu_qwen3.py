@@ -128,6 +128,24 @@ def test_prompt_attention_on_the_matrix_cores_equals_the_vector_path(gpu, name):
     assert np.abs(out[0] - out[1]).max() <= 2e-4 * (1 + np.abs(out[1]).max())
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(64, 8, 8), (64, 8, 2), (64, 16, 2), (128, 4, 4), (128, 16, 2)])
+def test_prompt_attention_equals_the_vector_path_at_every_group_size(gpu, head_dim, heads, kv_heads):
+    """The matrix-core prompt attention at group sizes 1, 4 and 8 (q heads per kv head) and both head sizes, where
+    the staging of its key/value tiles takes its other layouts: against the vector-ALU attention on the same model,
+    a 1100-token prompt (two chunks of 512 and one of 76, rows past 1024 positions split over spans)."""
+    shape = dict(golden("mini_f16kv")["shape"], layers=2, head_dim=head_dim, heads=heads, kv_heads=kv_heads)
+    prompt = o.synth_prompt(29, 1100, shape["vocab"]).tolist()
+    model = Qwen3(gpu, shape, seed=5)
+    out = []
+    try:
+        for fast in (True, False):
+            gpu.set_fast_attention(fast)
+            out.append(model.forward(prompt, model.new_cache(len(prompt) + 1, m.KvFormat.F16)))
+    finally:
+        gpu.set_fast_attention(True)
+    assert np.abs(out[0] - out[1]).max() <= 2e-4 * (1 + np.abs(out[1]).max())
+
+
 def agree_until_a_near_tie(got, exp, gaps, tie=1e-3):
     """Greedy sequences agree, or first differ at a step whose oracle top-1/top-2 gap is below `tie`."""
     for i, (a, b) in enumerate(zip(got, exp)):
