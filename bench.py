@@ -5,7 +5,8 @@
 A step is one greedy decode token: argmax of the last logits, then one pass of the token through 36 layers and the
 output head (int8 group-128 weights, f32 scales, f32 activations split to f16 hi/lo on the matrix cores, f32
 accumulation). Weights are random-init N(0, 0.02) generated and quantized on the device (no checkpoint); the prompt
-is 4096 uniform random ids, prefilled before timing. The timed region is exactly K steps between two stream
+is 4096 uniform random ids, prefilled before timing (`prefill_tok_s` times that prefill, after an untimed
+1100-token prompt on another cache has loaded every prompt kernel). The timed region is exactly K steps between two stream
 synchronizations, with every input already resident in HBM.
 
 One JSON line goes to stdout. `roofline` comes from measurements right after the timed region: profiled decode
@@ -588,6 +589,10 @@ def main() -> int:
     capacity = args.prompt + args.warmup + args.steps + args.profile_steps + 8
     cache = model.new_cache(capacity, fmt)
     prompt = np.random.default_rng(args.seed).integers(0, shape["vocab"], args.prompt, dtype=np.uint32)
+    # an untimed 1100-token prompt first, on a cache of its own: every prompt kernel (chunks of 512, spans past
+    # 1024 positions) is loaded and the scratch is allocated before the timed prefill
+    warm = min(1100, args.prompt)
+    model.forward(prompt[:warm], model.new_cache(warm + 1, fmt))
     gpu.synchronize()
     t = time.perf_counter()
     model.forward(prompt, cache)
