@@ -228,12 +228,13 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
         }
 
     // staging of one tile: chunk j of the tile (key or value row chunk), positions clamped to the visible ones.
-    // TRV (when the threads divide them evenly): the value chunks go in units of 4 consecutive positions x 8 head
-    // values per thread, transposed in registers and stored as 8 rows of 4 halves (8-byte stores) instead of 8
-    // single halves per chunk.
+    // TRV (when the threads divide them evenly): the value chunks go in units of VPU (4, else 2) consecutive
+    // positions x 8 head values per thread, transposed in registers and stored as 8 rows of VPU halves (8- or 4-byte
+    // stores) instead of 8 single halves per chunk.
     constexpr int CHUNKS = 2 * FA_TILE * CH;
     constexpr int SLOTS = (CHUNKS + NT - 1) / NT;
-    constexpr int KCH = FA_TILE * CH, VU = KCH / 4;  // key chunks, value units
+    constexpr int KCH = FA_TILE * CH;  // key chunks
+    constexpr int VPU = (KCH / 4) % NT == 0 ? 4 : 2, VU = KCH / VPU;  // positions per value unit, value units
     constexpr bool TRV = KCH % NT == 0 && VU % NT == 0;
     constexpr int KPT = KCH / NT, VPT = VU / NT;  // (TRV) key chunks and value units per thread
     u32x4 stage[SLOTS];
@@ -252,9 +253,9 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
             }
 #pragma unroll
             for (int v = 0; v < VPT; ++v) {
-                const int u = (int)threadIdx.x + v * NT, ch = u / (FA_TILE / 4), pg = u % (FA_TILE / 4);
+                const int u = (int)threadIdx.x + v * NT, ch = u / (FA_TILE / VPU), pg = u % (FA_TILE / VPU);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) stage[KPT + 4 * v + k] = load_chunk(1, 4 * pg + k, ch, p0);
+                for (int k = 0; k < VPU; ++k) stage[KPT + VPU * v + k] = load_chunk(1, VPU * pg + k, ch, p0);
             }
         } else {
 #pragma unroll
@@ -273,16 +274,19 @@ __global__ __launch_bounds__(64 * G) void fa_prefill(const _Float16 *__restrict_
             }
 #pragma unroll
             for (int v = 0; v < VPT; ++v) {
-                const int u = (int)threadIdx.x + v * NT, ch = u / (FA_TILE / 4), pg = u % (FA_TILE / 4);
-                const u32x4 *c4 = &stage[KPT + 4 * v];  // positions 4 pg .. + 3, head values 8 ch .. + 7
+                const int u = (int)threadIdx.x + v * NT, ch = u / (FA_TILE / VPU), pg = u % (FA_TILE / VPU);
+                const u32x4 *c4 = &stage[KPT + VPU * v];  // positions VPU pg .. + VPU - 1, head values 8 ch .. + 7
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int w = e / 2;
                     auto pair = [&](const u32x4 &a, const u32x4 &b) {  // half e of a (low), of b (high)
                         return (e & 1) ? (a[w] >> 16) | (b[w] & 0xffff0000u) : (a[w] & 0xffffu) | (b[w] << 16);
                     };
-                    *reinterpret_cast<uint2 *>(&vt[8 * ch + e][4 * pg]) =
-                        make_uint2(pair(c4[0], c4[1]), pair(c4[2], c4[3]));
+                    if constexpr (VPU == 4)
+                        *reinterpret_cast<uint2 *>(&vt[8 * ch + e][4 * pg]) =
+                            make_uint2(pair(c4[0], c4[1]), pair(c4[2], c4[3]));
+                    else
+                        *reinterpret_cast<uint32_t *>(&vt[8 * ch + e][2 * pg]) = pair(c4[0], c4[1]);
                 }
             }
         } else {
